@@ -1,0 +1,154 @@
+// C ABI of the gfx950 W8A8 Linear library (declared in include/d3w8a8.h).
+//
+// Every entry point validates its arguments on the host, so a kernel is only
+// ever launched on shapes, strides and alignments it was written for; a bad
+// argument returns D3W8A8_EINVAL with a message instead of reaching the GPU.
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "common.hpp"
+#include "kernels.hpp"
+#include "../../include/d3w8a8.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return D3W8A8_OK;
+  if (e == hipErrorInvalidValue) return fail(D3W8A8_EINVAL, "%s: unsupported argument combination", what);
+  return fail(D3W8A8_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool mode_ok(int m) { return m == D3W8A8_INT8 || m == D3W8A8_FP8; }
+bool dtype_ok(int d) { return d == D3W8A8_BF16 || d == D3W8A8_F16 || d == D3W8A8_F32; }
+int esize(int d) { return d == D3W8A8_F32 ? 4 : 2; }
+bool aligned(const void* p, int a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* d3w8a8_version(void) { return "d3w8a8 0.1.0 gfx950"; }
+
+const char* d3w8a8_last_error(void) { return g_err; }
+
+int d3w8a8_quantize_rows(int mode, int in_dtype, const void* x, int64_t ldx, int64_t M, int64_t K, void* q,
+                         int64_t ldq, float* scale, void* stream) {
+  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "quantize_rows: unknown mode %d", mode);
+  if (!dtype_ok(in_dtype)) return fail(D3W8A8_EINVAL, "quantize_rows: unknown dtype %d", in_dtype);
+  if (M < 0 || K < 1 || ldx < K || ldq < K) return fail(D3W8A8_EINVAL, "quantize_rows: bad shape M=%lld K=%lld ldx=%lld ldq=%lld", (long long)M, (long long)K, (long long)ldx, (long long)ldq);
+  if (M == 0) return D3W8A8_OK;
+  if (!x || !q || !scale) return fail(D3W8A8_EINVAL, "quantize_rows: null pointer");
+  const int es = esize(in_dtype);
+  const int va = es == 4 ? 32 : 16;  // bytes per 8 elements
+  const bool vec = K % 8 == 0 && (ldx * es) % va == 0 && aligned(x, va) && ldq % 8 == 0 && aligned(q, 8);
+  return hip_status(d3::launch_quant_rows(mode, in_dtype, x, ldx, M, K, q, ldq, scale, vec, (hipStream_t)stream),
+                    "quantize_rows");
+}
+
+int d3w8a8_rmsnorm_quantize(int mode, int in_dtype, const void* x, int64_t ldx, int w_dtype, const void* w,
+                            int64_t M, int64_t K, float eps, int zero_centered, void* q, int64_t ldq, float* scale,
+                            void* normed, int64_t ldn, float* clear_amax, void* stream) {
+  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "rmsnorm_quantize: unknown mode %d", mode);
+  if (!dtype_ok(in_dtype) || !dtype_ok(w_dtype)) return fail(D3W8A8_EINVAL, "rmsnorm_quantize: unknown dtype");
+  if (w_dtype != D3W8A8_F32 && w_dtype != in_dtype)
+    return fail(D3W8A8_EINVAL, "rmsnorm_quantize: weight dtype must be fp32 or the input dtype");
+  if (M < 0 || K < 8 || K % 8 != 0 || K > d3::kMaxVecK || ldx < K || ldq < K || (normed && ldn < K))
+    return fail(D3W8A8_EINVAL, "rmsnorm_quantize: bad shape M=%lld K=%lld (K must be a multiple of 8, <= %lld)",
+                (long long)M, (long long)K, (long long)d3::kMaxVecK);
+  if (M == 0) return D3W8A8_OK;
+  if (!x || !w || !q || !scale) return fail(D3W8A8_EINVAL, "rmsnorm_quantize: null pointer");
+  const int es = esize(in_dtype), va = es == 4 ? 32 : 16, vw = w_dtype == D3W8A8_F32 ? 32 : 16;
+  if ((ldx * es) % va || !aligned(x, va) || !aligned(w, vw) || ldq % 8 || !aligned(q, 8) ||
+      (normed && ((ldn * es) % va || !aligned(normed, va))))
+    return fail(D3W8A8_EINVAL, "rmsnorm_quantize: rows must be 16-byte aligned (32 for fp32)");
+  return hip_status(d3::launch_rmsnorm_quant(mode, in_dtype, w_dtype, x, ldx, w, M, K, eps, zero_centered ? 1 : 0, q,
+                                             ldq, scale, normed, ldn, clear_amax, (hipStream_t)stream),
+                    "rmsnorm_quantize");
+}
+
+int d3w8a8_quantize_rows_amax(int mode, int in_dtype, const void* h, int64_t ldh, const float* amax, int64_t M,
+                              int64_t K, void* q, int64_t ldq, float* scale, void* stream) {
+  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "quantize_rows_amax: unknown mode %d", mode);
+  if (!dtype_ok(in_dtype)) return fail(D3W8A8_EINVAL, "quantize_rows_amax: unknown dtype %d", in_dtype);
+  if (M < 0 || K < 8 || K % 8 != 0 || K > d3::kMaxVecK || ldh < K || ldq < K)
+    return fail(D3W8A8_EINVAL, "quantize_rows_amax: bad shape M=%lld K=%lld", (long long)M, (long long)K);
+  if (M == 0) return D3W8A8_OK;
+  if (!h || !amax || !q || !scale) return fail(D3W8A8_EINVAL, "quantize_rows_amax: null pointer");
+  const int es = esize(in_dtype), va = es == 4 ? 32 : 16;
+  if ((ldh * es) % va || !aligned(h, va) || ldq % 8 || !aligned(q, 8))
+    return fail(D3W8A8_EINVAL, "quantize_rows_amax: rows must be 16-byte aligned");
+  return hip_status(d3::launch_quant_rows_amax(mode, in_dtype, h, ldh, amax, M, K, q, ldq, scale, (hipStream_t)stream),
+                    "quantize_rows_amax");
+}
+
+int d3w8a8_quantize_rows_ragged(int mode, int in_dtype, const void* x, int64_t ldx, const int32_t* lengths,
+                                int64_t nseg, int64_t width, int64_t K, void* q, int64_t ldq, float* scale,
+                                int32_t* row_map, void* out, int out_dtype, int64_t ldo, int64_t N, void* stream) {
+  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "quantize_rows_ragged: unknown mode %d", mode);
+  if (!dtype_ok(in_dtype) || (out && !dtype_ok(out_dtype)))
+    return fail(D3W8A8_EINVAL, "quantize_rows_ragged: unknown dtype");
+  if (nseg < 0 || width < 0 || K < 8 || K % 8 != 0 || K > d3::kMaxVecK || ldx < K || ldq < K)
+    return fail(D3W8A8_EINVAL, "quantize_rows_ragged: bad shape nseg=%lld width=%lld K=%lld", (long long)nseg,
+                (long long)width, (long long)K);
+  if (nseg * width > INT32_MAX) return fail(D3W8A8_EINVAL, "quantize_rows_ragged: too many rows");
+  if (nseg == 0 || width == 0) return D3W8A8_OK;
+  if (!x || !lengths || !q || !scale || !row_map) return fail(D3W8A8_EINVAL, "quantize_rows_ragged: null pointer");
+  const int es = esize(in_dtype), va = es == 4 ? 32 : 16;
+  if ((ldx * es) % va || !aligned(x, va) || ldq % 8 || !aligned(q, 8))
+    return fail(D3W8A8_EINVAL, "quantize_rows_ragged: rows must be 16-byte aligned");
+  int oes = 2;
+  if (out) {
+    oes = esize(out_dtype);
+    if (N < 1 || ldo < N || (N * oes) % 16 || (ldo * oes) % 16 || !aligned(out, 16))
+      return fail(D3W8A8_EINVAL, "quantize_rows_ragged: output rows must be 16-byte multiples and aligned");
+  }
+  return hip_status(d3::launch_quant_ragged(mode, in_dtype, oes, x, ldx, lengths, nseg, width, K, q, ldq, scale,
+                                            row_map, out, ldo, N, (hipStream_t)stream),
+                    "quantize_rows_ragged");
+}
+
+int d3w8a8_gemm(int mode, const void* a, int64_t lda, const float* a_scale, const void* w, int64_t ldw,
+                const float* w_scale, int64_t M, int64_t N, int64_t K, int epilogue, int out_dtype, void* out,
+                int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
+                void* stream) {
+  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "gemm: unknown mode %d", mode);
+  if (epilogue < D3W8A8_EPI_DEQUANT || epilogue > D3W8A8_EPI_RESIDUAL)
+    return fail(D3W8A8_EINVAL, "gemm: unknown epilogue %d", epilogue);
+  if (epilogue != D3W8A8_EPI_RAW && !dtype_ok(out_dtype)) return fail(D3W8A8_EINVAL, "gemm: unknown out dtype");
+  if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_64x128) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
+  if (M < 0 || N < 0 || K < 0 || K % 16 != 0)
+    return fail(D3W8A8_EINVAL, "gemm: bad shape M=%lld N=%lld K=%lld (K must be a multiple of 16)", (long long)M,
+                (long long)N, (long long)K);
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2) return fail(D3W8A8_EINVAL, "gemm: M or N too large");
+  const int64_t ncols = epilogue == D3W8A8_EPI_SWIGLU ? N / 2 : N;
+  if (lda < K || ldw < K || lda % 16 || ldw % 16 || ldo < ncols)
+    return fail(D3W8A8_EINVAL, "gemm: leading dimensions must cover the rows and be multiples of 16");
+  if (M == 0 || N == 0) return D3W8A8_OK;
+  if (!a || !w || !out || (epilogue != D3W8A8_EPI_RAW && (!a_scale || !w_scale)))
+    return fail(D3W8A8_EINVAL, "gemm: null pointer");
+  if (!aligned(a, 16) || !aligned(w, 16)) return fail(D3W8A8_EINVAL, "gemm: operands must be 16-byte aligned");
+  if (epilogue == D3W8A8_EPI_SWIGLU) {
+    if (N % 64 != 0) return fail(D3W8A8_EINVAL, "gemm: swiglu needs N %% 64 == 0 (interleaved gate/up)");
+    if (row_map) return fail(D3W8A8_EINVAL, "gemm: swiglu output stays in GEMM row order (no row_map)");
+  }
+  if (epilogue == D3W8A8_EPI_RESIDUAL && (!res || ldr < N)) return fail(D3W8A8_EINVAL, "gemm: residual missing");
+  d3::GemmParams p{};
+  p.a = (const uint8_t*)a; p.lda = lda; p.a_scale = a_scale;
+  p.w = (const uint8_t*)w; p.ldw = ldw; p.w_scale = w_scale;
+  p.M = M; p.N = N; p.K = K;
+  p.out = out; p.ldo = ldo; p.res = res; p.ldr = ldr;
+  p.row_amax = row_amax; p.row_map = row_map;
+  return hip_status(d3::launch_gemm(mode, p, epilogue, out_dtype, tile, (hipStream_t)stream), "gemm");
+}
+
+}  // extern "C"

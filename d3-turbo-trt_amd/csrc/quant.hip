@@ -1,0 +1,410 @@
+// Per-token quantization kernels for gfx950: plain, fused with RMSNorm,
+// from a precomputed row amax (after SwiGLU), and the ragged gather form.
+//
+// One 64-lane wave owns one row. A lane holds NCH chunks of 8 consecutive
+// elements (chunk c covers columns [512c, 512c+512); lane l holds columns
+// 512c + 8l .. +8), loaded with 128-bit loads, so the row is read from HBM
+// exactly once and the amax is a register + cross-lane reduction.
+//
+// Reference arithmetic: d3trt/model/quant.py:92-100 (quantize_rows) and
+// :77-89 (quantize_weight, the same per-row arithmetic over [N, K]);
+// RMSNorm is transformers' Qwen3_5RMSNorm (modeling_qwen3_5.py:720-734).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace d3 {
+
+constexpr int kQuantWaves = 4;  // rows per 256-thread block
+
+// 8 consecutive elements of dtype DT at p (16B-aligned for 16-bit types,
+// 32B-aligned for fp32) -> 8 floats.
+template <int DT>
+__device__ __forceinline__ void load8(const void* p, float* v) {
+  if constexpr (DT == kF32) {
+    const float4* q = (const float4*)p;
+    float4 a = q[0], b = q[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    uint4 u = *(const uint4*)p;
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == kBF16) {
+        v[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu);
+        v[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
+      } else {
+        v[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+        v[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+      }
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store8(void* p, const float* v) {
+  if constexpr (DT == kF32) {
+    float4* q = (float4*)p;
+    q[0] = make_float4(v[0], v[1], v[2], v[3]);
+    q[1] = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t lo, hi;
+      if constexpr (DT == kBF16) { lo = f32_to_bf16_bits(v[2 * i]); hi = f32_to_bf16_bits(v[2 * i + 1]); }
+      else { lo = f32_to_f16_bits(v[2 * i]); hi = f32_to_f16_bits(v[2 * i + 1]); }
+      w[i] = lo | (hi << 16);
+    }
+    *(uint4*)p = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// Quantize 8 values with a row scale and store 8 bytes at q.
+template <int MODE>
+__device__ __forceinline__ void quant_store8(void* q, const float* v, float scale) {
+  uint32_t lo, hi;
+  if constexpr (MODE == kInt8) {
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = (uint32_t)(quant_i8(v[i], scale) & 0xff);
+    lo = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    hi = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+  } else {
+    lo = quant_f8_pair(v[0], v[1], scale) | (quant_f8_pair(v[2], v[3], scale) << 16);
+    hi = quant_f8_pair(v[4], v[5], scale) | (quant_f8_pair(v[6], v[7], scale) << 16);
+  }
+  *(uint2*)q = make_uint2(lo, hi);
+}
+
+template <int MODE>
+__device__ __forceinline__ float scale_from_amax(float amax) {
+  amax = fmaxf(amax, kAmaxFloor);  // clamp_min(1e-12)
+  return amax / (MODE == kInt8 ? kInt8Max : kFp8Max);
+}
+
+// ---------------------------------------------------------------------------
+// quantize_rows: x [M, K] (ld ldx) -> q [M, K] (ld ldq) + scale [M]
+// Vector path: K % 8 == 0, rows 16B aligned; NCH = ceil(K / 512).
+// With row_map != nullptr (ragged gather), logical row r reads source row
+// src_row(r) computed from the segment lengths; see quant_rows_ragged.
+// ---------------------------------------------------------------------------
+template <int MODE, int DT, int NCH>
+__global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ x, int64_t ldx,
+                                                     int64_t M, int64_t K, void* __restrict__ q,
+                                                     int64_t ldq, float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+  if (row >= M) return;
+  constexpr int ES = DT == kF32 ? 4 : 2;
+  const char* xr = (const char*)x + row * ldx * ES;
+  float v[NCH][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col = (int64_t)c * 512 + lane * 8;
+    if (col < K) {
+      load8<DT>(xr + col * ES, v[c]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
+    }
+  }
+  amax = wave_max(amax);
+  const float s = scale_from_amax<MODE>(amax);
+  char* qr = (char*)q + row * ldq;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col = (int64_t)c * 512 + lane * 8;
+    if (col < K) quant_store8<MODE>(qr + col, v[c], s);
+  }
+  if (lane == 0) scale[row] = s;
+}
+
+// Generic path for any K / alignment: two passes over the row (amax, then quantize).
+template <int MODE, int DT>
+__global__ __launch_bounds__(256) void quant_rows_generic(const void* __restrict__ x, int64_t ldx,
+                                                         int64_t M, int64_t K, void* __restrict__ q,
+                                                         int64_t ldq, float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int64_t base = row * ldx;
+  float amax = 0.0f;
+  for (int64_t k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(load_elem<DT>(x, base + k)));
+  amax = wave_max(amax);
+  const float s = scale_from_amax<MODE>(amax);
+  uint8_t* qr = (uint8_t*)q + row * ldq;
+  for (int64_t k = lane; k < K; k += 64) {
+    const float xv = load_elem<DT>(x, base + k);
+    if constexpr (MODE == kInt8) qr[k] = (uint8_t)(quant_i8(xv, s) & 0xff);
+    else qr[k] = (uint8_t)(quant_f8_pair(xv, 0.0f, s) & 0xff);
+  }
+  if (lane == 0) scale[row] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Requantization with a known row amax (SwiGLU output h [M, K]).
+// ---------------------------------------------------------------------------
+template <int MODE, int DT, int NCH>
+__global__ __launch_bounds__(256) void quant_rows_amax_vec(const void* __restrict__ h, int64_t ldh,
+                                                          const float* __restrict__ amax_in, int64_t M,
+                                                          int64_t K, void* __restrict__ q, int64_t ldq,
+                                                          float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+  if (row >= M) return;
+  constexpr int ES = DT == kF32 ? 4 : 2;
+  const float s = scale_from_amax<MODE>(amax_in[row]);
+  const char* hr = (const char*)h + row * ldh * ES;
+  char* qr = (char*)q + row * ldq;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col = (int64_t)c * 512 + lane * 8;
+    if (col < K) {
+      float v[8];
+      load8<DT>(hr + col * ES, v);
+      quant_store8<MODE>(qr + col, v, s);
+    }
+  }
+  if (lane == 0) scale[row] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Fused zero-centred RMSNorm + per-token quantization.
+//   y = DT( (x * rstd) * g ),  g = 1 + w (zero_centered) or w,
+//   rstd = 1 / sqrt(sum(x*x) / K + eps)  (correctly rounded), then q(y).
+// Optional: normed output y, and clear_amax[row] = 0 (the SwiGLU amax
+// buffer of the same rows, so the next GEMM can atomically max into it).
+// ---------------------------------------------------------------------------
+template <int MODE, int DT, int DTW, int NCH>
+__global__ __launch_bounds__(256) void rmsnorm_quant_vec(
+    const void* __restrict__ x, int64_t ldx, const void* __restrict__ w, int64_t M, int64_t K,
+    float eps, int zero_centered, void* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+    void* __restrict__ normed, int64_t ldn, float* __restrict__ clear_amax) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+  if (row >= M) return;
+  constexpr int ES = DT == kF32 ? 4 : 2;
+  constexpr int ESW = DTW == kF32 ? 4 : 2;
+  const char* xr = (const char*)x + row * ldx * ES;
+  float v[NCH][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col = (int64_t)c * 512 + lane * 8;
+    if (col < K) {
+      load8<DT>(xr + col * ES, v[c]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float sq = v[c][i] * v[c][i];
+        ss = ss + sq;
+      }
+    }
+  }
+  ss = wave_sum_tree(ss);
+  const float var = ss / (float)K;
+  const float t = var + eps;
+  const float rstd = (float)(1.0 / sqrt((double)t));
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col = (int64_t)c * 512 + lane * 8;
+    if (col < K) {
+      float g[8];
+      load8<DTW>((const char*)w + col * ESW, g);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float gain = zero_centered ? (1.0f + g[i]) : g[i];
+        const float nx = v[c][i] * rstd;
+        const float y = round_to<DT>(nx * gain);
+        v[c][i] = y;
+        amax = fmaxf(amax, fabsf(y));
+      }
+    }
+  }
+  amax = wave_max(amax);
+  const float s = scale_from_amax<MODE>(amax);
+  char* qr = (char*)q + row * ldq;
+  char* nr = normed ? (char*)normed + row * ldn * ES : nullptr;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col = (int64_t)c * 512 + lane * 8;
+    if (col < K) {
+      quant_store8<MODE>(qr + col, v[c], s);
+      if (nr) store8<DT>(nr + col * ES, v[c]);
+    }
+  }
+  if (lane == 0) {
+    scale[row] = s;
+    if (clear_amax) clear_amax[row] = 0.0f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Ragged gather: x is the right-padded [nseg, width, K] question batch;
+// segment b holds lengths[b] valid rows. Valid row (b, t) is quantized into
+// packed row off(b) + t, off(b) = lengths[0] + ... + lengths[b-1], and
+// row_map[packed] = b * width + t. Padded rows (t >= lengths[b]) instead get
+// their output row zeroed (out [nseg*width, N] of out_dtype, ld ldo), so the
+// GEMM, which only visits packed rows, leaves a fully defined output.
+// ---------------------------------------------------------------------------
+template <int MODE, int DT, int NCH, int OUTES>
+__global__ __launch_bounds__(256) void quant_rows_ragged_vec(
+    const void* __restrict__ x, int64_t ldx, const int32_t* __restrict__ lengths, int64_t nseg,
+    int64_t width, int64_t K, void* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+    int32_t* __restrict__ row_map, void* __restrict__ out, int64_t ldo, int64_t N) {
+  const int lane = threadIdx.x & 63;
+  const int64_t prow = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+  if (prow >= nseg * width) return;
+  const int64_t b = prow / width, t = prow - b * width;
+  // offset of segment b: wave-parallel sum of lengths[0..b)
+  int64_t part = 0;
+  for (int64_t i = lane; i < b; i += 64) part += lengths[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+  const int64_t len = lengths[b];
+  if (t >= len) {
+    if (out) {
+      // the host guarantees 16-byte aligned output rows and N * OUTES % 16 == 0
+      char* orow = (char*)out + prow * ldo * OUTES;
+      for (int64_t byte = (int64_t)lane * 16; byte < N * OUTES; byte += 64 * 16)
+        *(uint4*)(orow + byte) = make_uint4(0, 0, 0, 0);
+    }
+    return;
+  }
+  const int64_t dst = part + t;
+  constexpr int ES = DT == kF32 ? 4 : 2;
+  const char* xr = (const char*)x + prow * ldx * ES;
+  float v[NCH][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col = (int64_t)c * 512 + lane * 8;
+    if (col < K) {
+      load8<DT>(xr + col * ES, v[c]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
+    }
+  }
+  amax = wave_max(amax);
+  const float s = scale_from_amax<MODE>(amax);
+  char* qr = (char*)q + dst * ldq;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col = (int64_t)c * 512 + lane * 8;
+    if (col < K) quant_store8<MODE>(qr + col, v[c], s);
+  }
+  if (lane == 0) {
+    scale[dst] = s;
+    row_map[dst] = (int32_t)prow;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
+#define D3_NCH_DISPATCH(K, FN)                                   \
+  do {                                                           \
+    const int64_t nch_ = ((K) + 511) / 512;                      \
+    if (nch_ <= 1) { FN(1); }                                    \
+    else if (nch_ <= 2) { FN(2); }                               \
+    else if (nch_ <= 4) { FN(4); }                               \
+    else if (nch_ <= 8) { FN(8); }                               \
+    else if (nch_ <= 12) { FN(12); }                             \
+    else if (nch_ <= 16) { FN(16); }                             \
+    else if (nch_ <= 24) { FN(24); }                             \
+    else { FN(32); }                                             \
+  } while (0)
+
+
+static inline dim3 quant_grid(int64_t rows) { return dim3((unsigned)((rows + kQuantWaves - 1) / kQuantWaves)); }
+
+template <int MODE, int DT>
+hipError_t launch_quant_rows_t(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int64_t ldq,
+                               float* scale, bool vec, hipStream_t st) {
+  if (M == 0) return hipSuccess;
+  if (vec && K <= kMaxVecK) {
+#define L(N) hipLaunchKernelGGL((quant_rows_vec<MODE, DT, N>), quant_grid(M), dim3(256), 0, st, x, ldx, M, K, q, ldq, scale)
+    D3_NCH_DISPATCH(K, L);
+#undef L
+  } else {
+    hipLaunchKernelGGL((quant_rows_generic<MODE, DT>), quant_grid(M), dim3(256), 0, st, x, ldx, M, K, q, ldq, scale);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_rows(int mode, int dt, const void* x, int64_t ldx, int64_t M, int64_t K, void* q,
+                             int64_t ldq, float* scale, bool vec, hipStream_t st) {
+#define C(MO, D) if (mode == MO && dt == D) return launch_quant_rows_t<MO, D>(x, ldx, M, K, q, ldq, scale, vec, st)
+  C(kInt8, kBF16); C(kInt8, kF16); C(kInt8, kF32);
+  C(kFp8, kBF16); C(kFp8, kF16); C(kFp8, kF32);
+#undef C
+  return hipErrorInvalidValue;
+}
+
+template <int MODE, int DT>
+hipError_t launch_quant_rows_amax_t(const void* h, int64_t ldh, const float* amax, int64_t M, int64_t K, void* q,
+                                    int64_t ldq, float* scale, hipStream_t st) {
+  if (M == 0) return hipSuccess;
+#define L(N) hipLaunchKernelGGL((quant_rows_amax_vec<MODE, DT, N>), quant_grid(M), dim3(256), 0, st, h, ldh, amax, M, K, q, ldq, scale)
+  D3_NCH_DISPATCH(K, L);
+#undef L
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_rows_amax(int mode, int dt, const void* h, int64_t ldh, const float* amax, int64_t M,
+                                  int64_t K, void* q, int64_t ldq, float* scale, hipStream_t st) {
+  if (K > kMaxVecK) return hipErrorInvalidValue;
+#define C(MO, D) if (mode == MO && dt == D) return launch_quant_rows_amax_t<MO, D>(h, ldh, amax, M, K, q, ldq, scale, st)
+  C(kInt8, kBF16); C(kInt8, kF16); C(kInt8, kF32);
+  C(kFp8, kBF16); C(kFp8, kF16); C(kFp8, kF32);
+#undef C
+  return hipErrorInvalidValue;
+}
+
+template <int MODE, int DT, int DTW>
+hipError_t launch_rmsnorm_quant_t(const void* x, int64_t ldx, const void* w, int64_t M, int64_t K, float eps,
+                                  int zc, void* q, int64_t ldq, float* scale, void* normed, int64_t ldn,
+                                  float* clear_amax, hipStream_t st) {
+  if (M == 0) return hipSuccess;
+#define L(N) hipLaunchKernelGGL((rmsnorm_quant_vec<MODE, DT, DTW, N>), quant_grid(M), dim3(256), 0, st, x, ldx, w, M, K, eps, zc, q, ldq, scale, normed, ldn, clear_amax)
+  D3_NCH_DISPATCH(K, L);
+#undef L
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_quant(int mode, int dt, int dtw, const void* x, int64_t ldx, const void* w, int64_t M,
+                                int64_t K, float eps, int zc, void* q, int64_t ldq, float* scale, void* normed,
+                                int64_t ldn, float* clear_amax, hipStream_t st) {
+  if (K > kMaxVecK) return hipErrorInvalidValue;
+#define C(MO, D, W) if (mode == MO && dt == D && dtw == W) return launch_rmsnorm_quant_t<MO, D, W>(x, ldx, w, M, K, eps, zc, q, ldq, scale, normed, ldn, clear_amax, st)
+  C(kInt8, kBF16, kBF16); C(kInt8, kBF16, kF32); C(kInt8, kF16, kF16); C(kInt8, kF16, kF32); C(kInt8, kF32, kF32);
+  C(kFp8, kBF16, kBF16); C(kFp8, kBF16, kF32); C(kFp8, kF16, kF16); C(kFp8, kF16, kF32); C(kFp8, kF32, kF32);
+#undef C
+  return hipErrorInvalidValue;
+}
+
+template <int MODE, int DT, int OUTES>
+hipError_t launch_quant_ragged_t(const void* x, int64_t ldx, const int32_t* lengths, int64_t nseg, int64_t width,
+                                 int64_t K, void* q, int64_t ldq, float* scale, int32_t* row_map, void* out,
+                                 int64_t ldo, int64_t N, hipStream_t st) {
+  const int64_t rows = nseg * width;
+  if (rows == 0) return hipSuccess;
+#define L(NC) hipLaunchKernelGGL((quant_rows_ragged_vec<MODE, DT, NC, OUTES>), quant_grid(rows), dim3(256), 0, st, x, ldx, lengths, nseg, width, K, q, ldq, scale, row_map, out, ldo, N)
+  D3_NCH_DISPATCH(K, L);
+#undef L
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_ragged(int mode, int dt, int out_es, const void* x, int64_t ldx, const int32_t* lengths,
+                               int64_t nseg, int64_t width, int64_t K, void* q, int64_t ldq, float* scale,
+                               int32_t* row_map, void* out, int64_t ldo, int64_t N, hipStream_t st) {
+  if (K > kMaxVecK) return hipErrorInvalidValue;
+#define C(MO, D, E) if (mode == MO && dt == D && out_es == E) return launch_quant_ragged_t<MO, D, E>(x, ldx, lengths, nseg, width, K, q, ldq, scale, row_map, out, ldo, N, st)
+  C(kInt8, kBF16, 2); C(kInt8, kBF16, 4); C(kInt8, kF16, 2); C(kInt8, kF16, 4); C(kInt8, kF32, 2); C(kInt8, kF32, 4);
+  C(kFp8, kBF16, 2); C(kFp8, kBF16, 4); C(kFp8, kF16, 2); C(kFp8, kF16, 4); C(kFp8, kF32, 2); C(kFp8, kF32, 4);
+#undef C
+  return hipErrorInvalidValue;
+}
+
+}  // namespace d3

@@ -1,0 +1,88 @@
+"""ctypes binding of libd3w8a8.so (the C ABI declared in include/d3w8a8.h).
+
+The library is loaded from this package directory; there is no fallback. If
+it is missing or fails to load, every entry point raises, so a GPU run can
+never silently take another path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libd3w8a8.so")
+
+OK, EINVAL, EHIP = 0, 1, 2
+INT8, FP8 = 0, 1
+BF16, F16, F32 = 0, 1, 2
+EPI_DEQUANT, EPI_RAW, EPI_SWIGLU, EPI_RESIDUAL = 0, 1, 2, 3
+TILE_AUTO, TILE_256, TILE_128, TILE_64x128 = -1, 0, 1, 2
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+
+# name -> argtypes (every entry point returns int status)
+SIGNATURES = {
+    "d3w8a8_quantize_rows": [_i32, _i32, _p, _i64, _i64, _i64, _p, _i64, _p, _p],
+    "d3w8a8_rmsnorm_quantize": [_i32, _i32, _p, _i64, _i32, _p, _i64, _i64, _f32, _i32, _p, _i64, _p, _p,
+                                _i64, _p, _p],
+    "d3w8a8_quantize_rows_amax": [_i32, _i32, _p, _i64, _p, _i64, _i64, _p, _i64, _p, _p],
+    "d3w8a8_quantize_rows_ragged": [_i32, _i32, _p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i32,
+                                    _i64, _i64, _p],
+    "d3w8a8_gemm": [_i32, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p, _i64, _p,
+                    _p, _i32, _p],
+}
+STRING_FUNCS = ("d3w8a8_version", "d3w8a8_last_error")
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class LibraryMissing(RuntimeError):
+    """The HIP library is not built or cannot be loaded."""
+
+
+def load() -> ctypes.CDLL:
+    """Load and type the library once; raise LibraryMissing if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise LibraryMissing(
+                    f"{LIB_PATH} is not built; run `python d3-turbo-trt_amd/build.py` "
+                    "(the W8A8 path has no non-HIP implementation)"
+                )
+            try:
+                lib = ctypes.CDLL(LIB_PATH)
+            except OSError as exc:  # pragma: no cover - depends on the ROCm install
+                raise LibraryMissing(f"cannot load {LIB_PATH}: {exc}") from exc
+            for name, argtypes in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = argtypes
+                fn.restype = ctypes.c_int
+            for name in STRING_FUNCS:
+                fn = getattr(lib, name)
+                fn.argtypes = []
+                fn.restype = ctypes.c_char_p
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Map a C-ABI status to the reference's exception types (ValueError / RuntimeError)."""
+    if rc == OK:
+        return
+    msg = load().d3w8a8_last_error().decode(errors="replace")
+    if rc == EINVAL:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")
+
+
+def version() -> str:
+    return load().d3w8a8_version().decode()

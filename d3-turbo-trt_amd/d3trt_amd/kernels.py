@@ -1,0 +1,232 @@
+"""Thin torch wrappers over the C ABI: allocate outputs, pass pointers, raise on errors.
+
+Every function requires CUDA (ROCm) tensors and enqueues on the current
+stream. There is no CPU implementation behind any of them.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+
+FP8 = torch.float8_e4m3fn
+_DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16, torch.float32: _lib.F32}
+_MODE = {"int8": _lib.INT8, "fp8": _lib.FP8}
+
+
+def qdtype(mode: str) -> torch.dtype:
+    return torch.int8 if mode == "int8" else FP8
+
+
+def mode_code(mode: str) -> int:
+    try:
+        return _MODE[mode]
+    except KeyError:
+        raise ValueError(f"quant mode must be 'int8' or 'fp8', got {mode!r}") from None
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DT[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; expected bfloat16, float16 or float32") from None
+
+
+def _gpu(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not t.is_cuda:
+        raise RuntimeError(
+            f"{name} is on {t.device}; the d3trt_amd W8A8 path runs only as HIP kernels on the GPU"
+        )
+    return t
+
+
+def _rows(t: torch.Tensor, name: str) -> torch.Tensor:
+    """2-D view with unit column stride (copying only if the layout needs it)."""
+    _gpu(t, name)
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+        t = t.contiguous()
+    return t
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def quantize_rows(x: torch.Tensor, mode: str) -> tuple[torch.Tensor, torch.Tensor]:
+    """[M, K] float -> (q [M, K] int8/e4m3fn, scale [M, 1] fp32)."""
+    x = _rows(x, "x")
+    M, K = x.shape
+    q = torch.empty(M, K, dtype=qdtype(mode), device=x.device)
+    s = torch.empty(M, 1, dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    rc = lib.d3w8a8_quantize_rows(mode_code(mode), dtype_code(x.dtype), x.data_ptr(), x.stride(0), M, K,
+                                  q.data_ptr(), K, s.data_ptr(), _stream(x))
+    _lib.check(rc, "quantize_rows")
+    return q, s
+
+
+def rmsnorm_quantize(x: torch.Tensor, weight: torch.Tensor, eps: float, mode: str, *,
+                     zero_centered: bool = True, want_normed: bool = False,
+                     clear_amax: Optional[torch.Tensor] = None):
+    """Fused RMSNorm + per-token quant. Returns (q, scale [M,1], normed or None)."""
+    x = _rows(x, "x")
+    M, K = x.shape
+    w = _gpu(weight, "weight").contiguous()
+    if w.shape != (K,):
+        raise ValueError(f"norm weight shape {tuple(w.shape)} does not match hidden size {K}")
+    q = torch.empty(M, K, dtype=qdtype(mode), device=x.device)
+    s = torch.empty(M, 1, dtype=torch.float32, device=x.device)
+    normed = torch.empty_like(x, memory_format=torch.contiguous_format) if want_normed else None
+    if clear_amax is not None and (clear_amax.numel() < M or clear_amax.dtype != torch.float32):
+        raise ValueError("clear_amax must be a float32 buffer of at least M entries")
+    lib = _lib.load()
+    rc = lib.d3w8a8_rmsnorm_quantize(
+        mode_code(mode), dtype_code(x.dtype), x.data_ptr(), x.stride(0), dtype_code(w.dtype), w.data_ptr(),
+        M, K, float(eps), 1 if zero_centered else 0, q.data_ptr(), K, s.data_ptr(), _ptr(normed),
+        K if normed is not None else 0, _ptr(clear_amax), _stream(x))
+    _lib.check(rc, "rmsnorm_quantize")
+    return q, s, normed
+
+
+def quantize_rows_amax(h: torch.Tensor, amax: torch.Tensor, mode: str):
+    """Quantize rows whose amax is already known (SwiGLU output)."""
+    h = _rows(h, "h")
+    M, K = h.shape
+    if amax.dtype != torch.float32 or amax.numel() < M:
+        raise ValueError("amax must be float32 with one entry per row")
+    q = torch.empty(M, K, dtype=qdtype(mode), device=h.device)
+    s = torch.empty(M, 1, dtype=torch.float32, device=h.device)
+    lib = _lib.load()
+    rc = lib.d3w8a8_quantize_rows_amax(mode_code(mode), dtype_code(h.dtype), h.data_ptr(), h.stride(0),
+                                       amax.data_ptr(), M, K, q.data_ptr(), K, s.data_ptr(), _stream(h))
+    _lib.check(rc, "quantize_rows_amax")
+    return q, s
+
+
+def quantize_rows_ragged(x: torch.Tensor, lengths: Sequence[int], mode: str, *,
+                         out: Optional[torch.Tensor] = None):
+    """Right-padded [B, W, K] -> packed (q [T, K], scale [T, 1], row_map [T] int32).
+
+    T = sum(lengths). When ``out`` ([B*W, N] view of the final output) is given,
+    its padded rows are zeroed.
+    """
+    _gpu(x, "x")
+    if x.dim() != 3:
+        raise ValueError(f"ragged input must be [blocks, width, K], got {tuple(x.shape)}")
+    B, W, K = x.shape
+    lengths = [int(n) for n in lengths]
+    if len(lengths) != B or any(n < 0 or n > W for n in lengths):
+        raise ValueError(f"lengths {lengths} do not fit a [{B}, {W}] batch")
+    x2 = x.reshape(B * W, K)
+    x2 = _rows(x2, "x")
+    T = sum(lengths)
+    dev = x.device
+    lens = torch.tensor(lengths, dtype=torch.int32).to(dev, non_blocking=False)
+    # at least one row so the pointers are valid when every block is empty (the kernel
+    # still runs to zero the padded output rows)
+    q = torch.empty(max(T, 1), K, dtype=qdtype(mode), device=dev)
+    s = torch.empty(max(T, 1), 1, dtype=torch.float32, device=dev)
+    row_map = torch.empty(max(T, 1), dtype=torch.int32, device=dev)
+    N = out.shape[1] if out is not None else 0
+    lib = _lib.load()
+    rc = lib.d3w8a8_quantize_rows_ragged(
+        mode_code(mode), dtype_code(x2.dtype), x2.data_ptr(), x2.stride(0), lens.data_ptr(), B, W, K,
+        q.data_ptr(), K, s.data_ptr(), row_map.data_ptr(), _ptr(out),
+        dtype_code(out.dtype) if out is not None else 0, out.stride(0) if out is not None else 0, N,
+        _stream(x2))
+    _lib.check(rc, "quantize_rows_ragged")
+    return q[:T], s[:T], row_map[:T], lens
+
+
+def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.Tensor,
+         w_scale: Optional[torch.Tensor], *, epilogue: int = _lib.EPI_DEQUANT,
+         out_dtype: torch.dtype = torch.bfloat16, out: Optional[torch.Tensor] = None,
+         residual: Optional[torch.Tensor] = None, row_amax: Optional[torch.Tensor] = None,
+         row_map: Optional[torch.Tensor] = None, tile: int = _lib.TILE_AUTO) -> torch.Tensor:
+    """W8A8 GEMM ``a @ w.T`` with a fused epilogue (see include/d3w8a8.h)."""
+    a = _rows(a, "a")
+    w = _rows(w, "w")
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"inner dimensions differ: a {tuple(a.shape)} vs w {tuple(w.shape)}")
+    if a.dtype != qdtype(mode) or w.dtype != qdtype(mode):
+        raise ValueError(f"{mode} GEMM wants {qdtype(mode)} operands, got {a.dtype} and {w.dtype}")
+    if epilogue == _lib.EPI_RAW:
+        odt = torch.int32 if mode == "int8" else torch.float32
+        ncols = N
+    else:
+        odt = out_dtype
+        ncols = N // 2 if epilogue == _lib.EPI_SWIGLU else N
+    if out is None:
+        rows = M
+        if row_map is not None:
+            raise ValueError("a row_map GEMM needs an explicit output tensor")
+        out = torch.empty(rows, ncols, dtype=odt, device=a.device)
+    else:
+        _gpu(out, "out")
+        if out.dtype != odt or out.dim() != 2 or out.stride(1) != 1 or out.shape[1] < ncols:
+            raise ValueError("output tensor has the wrong dtype or layout")
+        if row_map is None and out.shape[0] < M:
+            raise ValueError("output tensor has too few rows")
+    if residual is not None:
+        _gpu(residual, "residual")
+        if residual.dtype != odt or residual.dim() != 2 or residual.stride(1) != 1:
+            raise ValueError("residual must be a row-major tensor of the output dtype")
+        if residual.shape[0] < out.shape[0] or residual.shape[1] < N:
+            raise ValueError("residual is smaller than the output")
+    if row_amax is not None and (row_amax.dtype != torch.float32 or row_amax.numel() < M
+                                 or not row_amax.is_contiguous()):
+        raise ValueError("row_amax must be a contiguous float32 buffer with one entry per GEMM row")
+    if row_map is not None:
+        if row_map.dtype != torch.int32 or row_map.numel() != M:
+            raise ValueError("row_map must be int32 with one entry per GEMM row")
+    for t, name in ((a_scale, "a_scale"), (w_scale, "w_scale")):
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
+            raise ValueError(f"{name} must be contiguous float32")
+    if epilogue != _lib.EPI_RAW:
+        if a_scale is None or w_scale is None or a_scale.numel() != M or w_scale.numel() != N:
+            raise ValueError("dequantizing epilogues need a_scale [M] and w_scale [N]")
+    lib = _lib.load()
+    rc = lib.d3w8a8_gemm(
+        mode_code(mode), a.data_ptr(), a.stride(0), _ptr(a_scale), w.data_ptr(), w.stride(0), _ptr(w_scale),
+        M, N, K, epilogue, dtype_code(odt) if epilogue != _lib.EPI_RAW else 0, out.data_ptr(), out.stride(0),
+        _ptr(residual), residual.stride(0) if residual is not None else 0, _ptr(row_amax), _ptr(row_map),
+        tile, _stream(a))
+    _lib.check(rc, "gemm")
+    return out
+
+
+def interleave_gate_up(full: torch.Tensor) -> torch.Tensor:
+    """Row permutation [gate; up] (the reference's cat layout, trtllm_stack.py:366-368)
+    -> blocks of 32: [g0..g31, u0..u31, g32..g63, u32..u63, ...].
+
+    Works on any tensor whose first dimension is 2*I with I % 32 == 0 (weights [2I, K]
+    or per-channel scales [2I]).
+    """
+    two_i = full.shape[0]
+    if two_i % 64:
+        raise ValueError(f"gate_up rows {two_i} must be a multiple of 64 for the SwiGLU layout")
+    i = two_i // 2
+    rest = full.shape[1:]
+    gate = full[:i].reshape(i // 32, 32, *rest)
+    up = full[i:].reshape(i // 32, 32, *rest)
+    return torch.stack([gate, up], dim=1).reshape(two_i, *rest).contiguous()
+
+
+def deinterleave_gate_up(inter: torch.Tensor) -> torch.Tensor:
+    """Inverse of :func:`interleave_gate_up`."""
+    two_i = inter.shape[0]
+    i = two_i // 2
+    rest = inter.shape[1:]
+    blocks = inter.reshape(i // 32, 2, 32, *rest)
+    return torch.cat([blocks[:, 0].reshape(i, *rest), blocks[:, 1].reshape(i, *rest)], dim=0).contiguous()

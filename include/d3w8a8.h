@@ -1,0 +1,110 @@
+/* d3w8a8 -- gfx950 (MI355X) W8A8 quantized Linear kernels behind a plain C ABI.
+ *
+ * The reference's boundary for this path is a Python module API, not an FFI:
+ * d3trt/model/quant.py (quantize_rows :92-100, quantize_weight :77-89,
+ * QuantLinear._int8 :190-197, QuantLinear._fp8 :164-188) and the MLP chain
+ * around it (trtllm_stack.py:131-134, core.py:214-215). Each entry point below
+ * replaces one of those torch call sequences; the Python mirror of the module
+ * (d3trt_amd.quant) binds them with ctypes.
+ *
+ * Conventions
+ *   - All pointers are device pointers owned by the caller; the library never
+ *     allocates. Matrices are row-major with explicit leading dimensions in
+ *     elements. Work is enqueued on `stream` (a hipStream_t; NULL = default
+ *     stream) and nothing synchronizes.
+ *   - Return 0 on success; D3W8A8_EINVAL for a bad mode/dtype/shape/stride/
+ *     alignment (the Python layer raises ValueError), D3W8A8_EHIP for a HIP
+ *     launch failure (RuntimeError). d3w8a8_last_error() returns the message of
+ *     the calling thread's last failure.
+ *   - Stateless and reentrant: concurrent calls on different streams are safe.
+ */
+#ifndef D3W8A8_H
+#define D3W8A8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define D3W8A8_OK 0
+#define D3W8A8_EINVAL 1
+#define D3W8A8_EHIP 2
+
+/* modes (quant.py:28 "fp8" / "int8") */
+#define D3W8A8_INT8 0
+#define D3W8A8_FP8 1
+
+/* element types of floating-point tensors */
+#define D3W8A8_BF16 0
+#define D3W8A8_F16 1
+#define D3W8A8_F32 2
+
+/* GEMM epilogues */
+#define D3W8A8_EPI_DEQUANT 0  /* out = OUT((float(acc) * a_scale[m]) * w_scale[n])      quant.py:162,197 */
+#define D3W8A8_EPI_RAW 1      /* out = acc: int32 (INT8) or fp32 (FP8)                 parity hook      */
+#define D3W8A8_EPI_SWIGLU 2   /* h = OUT(OUT(silu(g)) * u), g/u dequantized; row amax  trtllm_stack.py:131-134 */
+#define D3W8A8_EPI_RESIDUAL 3 /* out = OUT(res + OUT(dequant))                         core.py:215      */
+
+/* GEMM tile configurations (D3W8A8_TILE_AUTO picks one from M and N) */
+#define D3W8A8_TILE_AUTO (-1)
+#define D3W8A8_TILE_256 0
+#define D3W8A8_TILE_128 1
+#define D3W8A8_TILE_64x128 2
+
+const char* d3w8a8_version(void);
+const char* d3w8a8_last_error(void);
+
+/* Per-token dynamic quantization.
+ * Replaces quant.py:92-100 quantize_rows(x, mode) and, applied to a weight
+ * [N, K], quant.py:77-89 quantize_weight (same per-row arithmetic).
+ *   x [M, K] (in_dtype, ld ldx) -> q [M, K] int8 / e4m3fn (ld ldq), scale [M] fp32
+ *   scale = max(max|x_m|, 1e-12) / (127 | 448); q = clamp(rne(x / scale)) */
+int d3w8a8_quantize_rows(int mode, int in_dtype, const void* x, int64_t ldx, int64_t M, int64_t K,
+                         void* q, int64_t ldq, float* scale, void* stream);
+
+/* Fused zero-centred RMSNorm + per-token quantization.
+ * Replaces the input/post-attention RMSNorm (trtllm_stack.py:217-228,
+ * Qwen3_5RMSNorm semantics) followed by quant.py:92-100 on its output.
+ *   y = in_dtype((x * rsqrt(mean(x^2) + eps)) * (zero_centered ? 1 + w : w)); q, scale = quant(y)
+ * normed (optional, ld ldn) receives y; clear_amax (optional) gets clear_amax[m] = 0
+ * for every row, preparing the SwiGLU epilogue's row-amax buffer. */
+int d3w8a8_rmsnorm_quantize(int mode, int in_dtype, const void* x, int64_t ldx, int w_dtype, const void* w,
+                            int64_t M, int64_t K, float eps, int zero_centered, void* q, int64_t ldq,
+                            float* scale, void* normed, int64_t ldn, float* clear_amax, void* stream);
+
+/* Quantization with the row amax already known (SwiGLU output h, amax from
+ * the SwiGLU epilogue): the quant.py:95-100 arithmetic after the amax. */
+int d3w8a8_quantize_rows_amax(int mode, int in_dtype, const void* h, int64_t ldh, const float* amax,
+                              int64_t M, int64_t K, void* q, int64_t ldq, float* scale, void* stream);
+
+/* Ragged gather-quantize for a right-padded question batch x [nseg, width, K]
+ * (backends/trtllm.py:149-179 builds such batches; core.py:158-181 runs them):
+ * valid row (b, t < lengths[b]) is quantized into packed row off(b) + t with
+ * row_map[off(b) + t] = b * width + t; padded rows of `out` (optional,
+ * [nseg * width, N] of out_dtype, ld ldo) are zeroed. lengths is a device
+ * int32 array of nseg entries. */
+int d3w8a8_quantize_rows_ragged(int mode, int in_dtype, const void* x, int64_t ldx, const int32_t* lengths,
+                                int64_t nseg, int64_t width, int64_t K, void* q, int64_t ldq, float* scale,
+                                int32_t* row_map, void* out, int out_dtype, int64_t ldo, int64_t N,
+                                void* stream);
+
+/* W8A8 GEMM with a fused epilogue. Replaces quant.py:196-197 (torch._int_mm +
+ * dequant) and quant.py:171-177 (torch._scaled_mm rowwise).
+ *   a [M, K] quantized activations (ld lda), a_scale [M]; w [N, K] quantized
+ *   weights (ld ldw), w_scale [N]; out per `epilogue` (ld ldo; N/2 columns for
+ *   SWIGLU); res (RESIDUAL only, ld ldr, out_dtype); row_amax [M] (SWIGLU,
+ *   atomically max-ed, must start at 0 or a lower bound); row_map [M]
+ *   (optional; output row of GEMM row m, from d3w8a8_quantize_rows_ragged).
+ * Requirements: K % 16 == 0; lda, ldw % 16 == 0; a, w 16-byte aligned;
+ * SWIGLU needs N % 64 == 0 with weights interleaved in blocks of 32 rows. */
+int d3w8a8_gemm(int mode, const void* a, int64_t lda, const float* a_scale, const void* w, int64_t ldw,
+                const float* w_scale, int64_t M, int64_t N, int64_t K, int epilogue, int out_dtype, void* out,
+                int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
+                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* D3W8A8_H */

@@ -1,0 +1,119 @@
+"""CPU: host-side API behaviour and the C-ABI library surface (no compute without a GPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from d3trt_amd import _lib, quant
+from tests.conftest import ROOT
+
+
+def test_shape_checks():
+    # reference tests/test_quant.py:53-60
+    assert quant.quantizable(5120, 17408)
+    assert not quant.quantizable(5120, 40)
+    with pytest.raises(ValueError):
+        quant.QuantLinear(64, 40, mode="fp8", dtype=torch.bfloat16, device="cpu")
+    layer = quant.QuantLinear(64, 32, mode="fp8", dtype=torch.bfloat16, device="cpu")
+    with pytest.raises(ValueError):
+        layer.load_full(torch.zeros(32, 48))
+
+
+def test_resolve_mode_off_gpu():
+    # reference tests/test_quant.py:63-68
+    assert quant.resolve_mode("auto", "cpu") == "none"
+    assert quant.resolve_mode("int8", "cpu") == "int8"
+    assert quant.resolve_mode("fp8", "cpu") == "fp8"
+    with pytest.raises(ValueError):
+        quant.resolve_mode("nvfp4", "cpu")
+
+
+def test_summarize_counts_quantized_bytes():
+    # reference tests/test_quant.py:71-80
+    layers = torch.nn.ModuleList(
+        [
+            quant.QuantLinear(64, 32, mode="int8", dtype=torch.float32, device="cpu"),
+            torch.nn.Linear(64, 8, bias=False),
+        ]
+    )
+    report = quant.summarize(layers.modules())
+    assert report["kernels"] == {"unused": 1}
+    assert report["quantized_gib"] == round(64 * 32 / 1024**3, 3)
+
+
+def test_constructor_errors_and_buffers():
+    with pytest.raises(ValueError):
+        quant.QuantLinear(64, 32, mode="none", dtype=torch.bfloat16, device="cpu")
+    layer = quant.QuantLinear(64, 32, mode="fp8", dtype=torch.bfloat16, device="cpu")
+    assert layer.weight.dtype == torch.float8_e4m3fn and layer.weight.shape == (32, 64)
+    assert layer.weight_scale.dtype == torch.float32 and torch.all(layer.weight_scale == 1)
+    assert layer.tp_size == 1 and layer.kernel is None
+    assert "weight" in dict(layer.named_buffers()) and "weight_scale" in dict(layer.named_buffers())
+    assert repr(layer) == "QuantLinear(in=64, out=32, mode=fp8)"
+
+
+def test_cpu_tensors_raise_instead_of_falling_back():
+    layer = quant.QuantLinear(64, 32, mode="int8", dtype=torch.bfloat16, device="cpu")
+    with pytest.raises(RuntimeError, match="HIP"):
+        layer(torch.zeros(2, 64, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="HIP"):
+        quant.quantize_rows(torch.zeros(2, 64), "int8")
+    with pytest.raises(RuntimeError, match="HIP"):
+        layer.load_full(torch.zeros(32, 64))
+
+
+def test_make_linear_dense_branch_on_cpu():
+    dense = quant.make_linear(64, 40, quant="int8", dtype=torch.float32, mapping=None,
+                              tensor_parallel_mode=None, device="cpu")
+    assert isinstance(dense, torch.nn.Linear) and dense.bias is None and dense.tp_size == 1
+    q = quant.make_linear(64, 32, quant="fp8", dtype=torch.bfloat16, mapping=None,
+                          tensor_parallel_mode=None, device="cpu")
+    assert isinstance(q, quant.QuantLinear)
+
+
+def _header_functions():
+    text = open(os.path.join(ROOT, "include", "d3w8a8.h")).read()
+    return re.findall(r"^\S.*?\b(d3w8a8_\w+)\s*\(", text, flags=re.M)
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    names = _header_functions()
+    assert set(names) == set(_lib.SIGNATURES) | set(_lib.STRING_FUNCS)
+    for name in names:
+        assert hasattr(lib, name), name
+    assert "gfx950" in _lib.version()
+
+
+def test_c_abi_rejects_bad_arguments_before_any_launch():
+    lib = _lib.load()
+    # unknown mode / dtype / epilogue and bad shapes return EINVAL on the host
+    assert lib.d3w8a8_quantize_rows(7, 0, None, 16, 1, 16, None, 16, None, None) == _lib.EINVAL
+    assert b"mode" in lib.d3w8a8_last_error()
+    assert lib.d3w8a8_quantize_rows(0, 9, None, 16, 1, 16, None, 16, None, None) == _lib.EINVAL
+    assert lib.d3w8a8_gemm(0, None, 24, None, None, 24, None, 4, 8, 24, 1, 0, None, 8, None, 0, None, None,
+                           -1, None) == _lib.EINVAL
+    assert b"multiple of 16" in lib.d3w8a8_last_error()
+    assert lib.d3w8a8_gemm(0, None, 32, None, None, 32, None, 4, 8, 32, 9, 0, None, 8, None, 0, None, None,
+                           -1, None) == _lib.EINVAL
+    assert lib.d3w8a8_rmsnorm_quantize(0, 0, None, 20, 0, None, 4, 20, 1e-6, 1, None, 20, None, None, 0,
+                                       None, None) == _lib.EINVAL
+    # empty problems are a successful no-op
+    assert lib.d3w8a8_quantize_rows(0, 0, None, 16, 0, 16, None, 16, None, None) == _lib.OK
+    with pytest.raises(ValueError):
+        _lib.check(_lib.EINVAL, "probe")
+
+
+def test_gate_up_interleave_roundtrip():
+    from d3trt_amd import kernels as K
+    w = torch.arange(128 * 3).reshape(128, 3)
+    il = K.interleave_gate_up(w)
+    assert torch.equal(il[:32], w[:32]) and torch.equal(il[32:64], w[64:96])
+    assert torch.equal(K.deinterleave_gate_up(il), w)
+    with pytest.raises(ValueError):
+        K.interleave_gate_up(torch.zeros(96, 2))
