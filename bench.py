@@ -190,6 +190,29 @@ def cpu_baseline_state_pass(layers, mode: str, rows: int):
     }
 
 
+def single_pass(mode: str) -> int:
+    """One plain copy of known size (64 MiB read + 64 MiB written, the counter calibration) and
+    then one step of the workload, for hardware-counter runs that count per dispatch."""
+    import torch
+
+    from d3trt_amd import _lib
+    from d3trt_amd import kernels as KK
+
+    dev = torch.device("cuda:0")
+    src = torch.ones(64 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    layers = build_state_pass(mode, dev)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    for _, M, N, K, x, lin in layers:
+        q, s = KK.quantize_rows(x, mode)
+        KK.gemm(mode, q, s.view(-1), lin.weight, lin.weight_scale, epilogue=_lib.EPI_DEQUANT,
+                out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    print(json.dumps({"single_pass": mode, "copy_bytes": src.numel()}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -198,6 +221,8 @@ def main() -> int:
     ap.add_argument("--mode", choices=["fp8", "int8"], default="fp8")
     ap.add_argument("--cpu-rows", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--single", action="store_true",
+                    help="run one untimed step after a 64 MiB copy (for rocprofv3 --pmc passes)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -210,6 +235,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU available"}))
         return 2
+    if args.single:
+        return single_pass(args.mode)
     result, layers = run_state_pass(args, args.mode)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_state_pass(layers, args.mode, args.cpu_rows)

@@ -125,7 +125,9 @@ int d3w8a8_gemm(int mode, const void* a, int64_t lda, const float* a_scale, cons
   if (epilogue < D3W8A8_EPI_DEQUANT || epilogue > D3W8A8_EPI_RESIDUAL)
     return fail(D3W8A8_EINVAL, "gemm: unknown epilogue %d", epilogue);
   if (epilogue != D3W8A8_EPI_RAW && !dtype_ok(out_dtype)) return fail(D3W8A8_EINVAL, "gemm: unknown out dtype");
-  if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_64x128) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
+  if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_256x128_W4) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
+  if (tile >= D3W8A8_TILE_DMA_256_W8 && K % 64 != 0)
+    return fail(D3W8A8_EINVAL, "gemm: the pipelined tiles need K %% 64 == 0");
   if (M < 0 || N < 0 || K < 0 || K % 16 != 0)
     return fail(D3W8A8_EINVAL, "gemm: bad shape M=%lld N=%lld K=%lld (K must be a multiple of 16)", (long long)M,
                 (long long)N, (long long)K);

@@ -46,11 +46,17 @@ extern "C" {
 #define D3W8A8_EPI_SWIGLU 2   /* h = OUT(OUT(silu(g)) * u), g/u dequantized; row amax  trtllm_stack.py:131-134 */
 #define D3W8A8_EPI_RESIDUAL 3 /* out = OUT(res + OUT(dequant))                         core.py:215      */
 
-/* GEMM tile configurations (D3W8A8_TILE_AUTO picks one from M and N) */
+/* GEMM tile configurations (D3W8A8_TILE_AUTO picks one from M, N and K).
+ * REG tiles stage K through registers and accept any K % 16 == 0; DMA tiles
+ * use the direct global->LDS pipeline and need K % 64 == 0. */
 #define D3W8A8_TILE_AUTO (-1)
-#define D3W8A8_TILE_256 0
-#define D3W8A8_TILE_128 1
-#define D3W8A8_TILE_64x128 2
+#define D3W8A8_TILE_256 0           /* REG 256x256, 4 waves */
+#define D3W8A8_TILE_128 1           /* REG 128x128, 4 waves */
+#define D3W8A8_TILE_64x128 2        /* REG 64x128, 4 waves */
+#define D3W8A8_TILE_DMA_256_W8 3    /* DMA 256x256, 8 waves */
+#define D3W8A8_TILE_DMA_256_W4 4    /* DMA 256x256, 4 waves */
+#define D3W8A8_TILE_DMA_128_W4 5    /* DMA 128x128, 4 waves */
+#define D3W8A8_TILE_DMA_256x128_W4 6 /* DMA 256x128, 4 waves */
 
 const char* d3w8a8_version(void);
 const char* d3w8a8_last_error(void);

@@ -24,7 +24,7 @@ def _swiglu_case(g, M, H, I, mode):
 
 
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
-@pytest.mark.parametrize("tile", [_lib.TILE_256, _lib.TILE_128, _lib.TILE_64x128])
+@pytest.mark.parametrize("tile", list(_lib.TILES))
 @pytest.mark.parametrize("M,H,I", [(96, 512, 256), (300, 1024, 1024)])
 def test_swiglu_epilogue(dev, mode, tile, M, H, I):
     g = gen(M + H + I)
@@ -48,7 +48,7 @@ def test_swiglu_epilogue(dev, mode, tile, M, H, I):
     assert torch.equal(amax.cpu(), h.float().abs().amax(dim=1))
 
 
-@pytest.mark.parametrize("tile", [_lib.TILE_256, _lib.TILE_128, _lib.TILE_64x128])
+@pytest.mark.parametrize("tile", list(_lib.TILES))
 def test_residual_epilogue_int8_bit_exact(dev, tile):
     g = gen(99)
     M, N, Kd = 130, 640, 1536

@@ -21,8 +21,19 @@ from d3trt_amd import kernels as K
 
 pytestmark = pytest.mark.gpu
 
-TILES = [_lib.TILE_256, _lib.TILE_128, _lib.TILE_64x128]
-SHAPES = [(1, 16, 16), (33, 80, 48), (128, 1024, 1024), (255, 192, 1040), (300, 520, 4096), (64, 4096, 272)]
+TILES = list(_lib.TILES)
+
+
+def _dma_needs_k64(tile, Kd, a, w) -> bool:
+    """The pipelined (DMA) tiles take K % 64 == 0 only; other K must be refused, not computed."""
+    if tile in _lib.DMA_TILES and Kd % 64:
+        mode = "int8" if a.dtype == torch.int8 else "fp8"
+        with pytest.raises(ValueError, match="K % 64"):
+            K.gemm(mode, a.to("cuda"), None, w.to("cuda"), None, epilogue=_lib.EPI_RAW, tile=tile)
+        return True
+    return False
+SHAPES = [(1, 16, 16), (33, 80, 48), (128, 1024, 1024), (255, 192, 1040), (300, 520, 4096), (64, 4096, 272),
+          (257, 300, 192), (513, 1000, 640)]
 
 
 @pytest.mark.parametrize("tile", TILES)
@@ -30,6 +41,8 @@ SHAPES = [(1, 16, 16), (33, 80, 48), (128, 1024, 1024), (255, 192, 1040), (300, 
 def test_int8_raw_accumulators_exact(dev, tile, M, N, Kd):
     g = gen(M * 131 + N * 7 + Kd)
     a, w = rand_i8(g, M, Kd), rand_i8(g, N, Kd)
+    if _dma_needs_k64(tile, Kd, a, w):
+        return
     acc = K.gemm("int8", a.to(dev), None, w.to(dev), None, epilogue=_lib.EPI_RAW, tile=tile)
     ref = R.int_accumulate(a, w)
     assert torch.equal(acc.cpu().to(torch.int64), ref)
@@ -60,6 +73,8 @@ def test_int8_dequant_bit_exact(dev, out_dtype, tile):
 def test_fp8_raw_accumulators(dev, tile, M, N, Kd):
     g = gen(M * 13 + N + Kd)
     a, w = rand_fp8(g, M, Kd), rand_fp8(g, N, Kd)
+    if _dma_needs_k64(tile, Kd, a, w):
+        return
     acc = K.gemm("fp8", a.to(dev), None, w.to(dev), None, epilogue=_lib.EPI_RAW, tile=tile).cpu()
     ref = R.fp8_accumulate(a, w)
     # MFMA FP8 accumulation: held to 2**-14 of the sum of |products|, element-wise
@@ -86,21 +101,22 @@ def test_fp8_dequant_within_tolerance(dev, tile):
 C2_SHAPES = [(4096, 6144, 4096), (4096, 4096, 4096), (4096, 24576, 4096), (4096, 4096, 12288)]
 
 
+@pytest.mark.parametrize("tile", [_lib.TILE_AUTO, *_lib.DMA_TILES])
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
 @pytest.mark.parametrize("M,N,Kd", C2_SHAPES)
-def test_state_pass_shapes_sampled(dev, mode, M, N, Kd):
+def test_state_pass_shapes_sampled(dev, mode, M, N, Kd, tile):
     g = gen(N + Kd)
     x = R.outlier_activations(g, M, Kd)
     wq, ws = R.quantize_weight(R.gaussian_weight(g, N, Kd), mode)
     q, s = K.quantize_rows(x.to(dev), mode)
-    out = K.gemm(mode, q, s.reshape(-1), wq.to(dev), ws.to(dev))
+    out = K.gemm(mode, q, s.reshape(-1), wq.to(dev), ws.to(dev), tile=tile)
     rows = torch.randperm(M, generator=g)[:48]
     rows = torch.cat([rows, torch.tensor([0, M - 1])])
     qs, ss = R.quantize_rows(x[rows], mode)
     assert torch.equal(q.cpu()[rows].view(torch.uint8), qs.view(torch.uint8))
     if mode == "int8":
         acc = R.int_accumulate(qs, wq)
-        raw = K.gemm(mode, q, None, wq.to(dev), None, epilogue=_lib.EPI_RAW)
+        raw = K.gemm(mode, q, None, wq.to(dev), None, epilogue=_lib.EPI_RAW, tile=tile)
         assert torch.equal(raw.cpu()[rows].to(torch.int64), acc)
         assert torch.equal(out.cpu()[rows], R.dequant(acc, ss, ws, torch.bfloat16))
     else:
