@@ -128,6 +128,9 @@ int d3w8a8_gemm(int mode, const void* a, int64_t lda, const float* a_scale, cons
   if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_256x128_W4) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
   if (tile >= D3W8A8_TILE_DMA_256_W8 && K % 64 != 0)
     return fail(D3W8A8_EINVAL, "gemm: the pipelined tiles need K %% 64 == 0");
+  if (tile >= D3W8A8_TILE_DMA_256_W8 && ((M > 0 && (M - 1) * lda + K >= ((int64_t)1 << 32)) ||
+                                         (N > 0 && (N - 1) * ldw + K >= ((int64_t)1 << 32))))
+    return fail(D3W8A8_EINVAL, "gemm: the pipelined tiles address each operand with 32-bit offsets");
   if (M < 0 || N < 0 || K < 0 || K % 16 != 0)
     return fail(D3W8A8_EINVAL, "gemm: bad shape M=%lld N=%lld K=%lld (K must be a multiple of 16)", (long long)M,
                 (long long)N, (long long)K);

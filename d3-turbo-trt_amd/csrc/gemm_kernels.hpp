@@ -1,0 +1,693 @@
+// W8A8 GEMM for gfx950: out[m, n] = epilogue( sum_k a[m, k] * w[n, k] ).
+//
+// Both operands are K-contiguous 8-bit matrices (a: per-token quantized
+// activations [M, K]; w: per-output-channel quantized weights [N, K]), the
+// "TN" product the reference asks of torch._int_mm / torch._scaled_mm
+// (d3trt/model/quant.py:171-177, 196).
+//
+// Structure (one workgroup = one BM x BN output tile):
+//   * K advances in steps of 128 bytes; A and B tiles of the step are staged
+//     in LDS, double-buffered: the global loads of step t+1 are in flight
+//     (128-bit, 8 lanes per 128-byte row segment) while the MFMAs of step t
+//     run, so there is one barrier per step.
+//   * LDS rows are 128 bytes; the 16-byte chunk c of row r is stored at chunk
+//     c ^ ((r >> 1) & 7), so the 16 lanes a ds_read_b128 serves per cycle (16
+//     consecutive rows, one chunk each) hit 16 distinct 16-byte bank groups.
+//   * WM x WN waves; each owns a (BM/WM) x (BN/WN) sub-tile made of 32x32
+//     MFMA blocks: v_mfma_i32_32x32x32_i8 (INT8) or
+//     v_mfma_scale_f32_32x32x64_f8f6f4 with format E4M3 and unit scales (FP8).
+//     Operand lane l carries row (l & 31) and the K chunk selected by l >> 5;
+//     A and B use the same K assignment, so the dot product is complete.
+//   * Result lane layout (32x32 blocks): register r of lane l is
+//     row 8*(r/4) + 4*(l/32) + (r%4), column l%32.
+//   * Workgroups are remapped so that each XCD (the hardware deals
+//     workgroups round-robin over 8 XCDs) receives a contiguous run of tiles,
+//     ordered in groups of GROUP_M tile-rows, so concurrently running tiles on
+//     one XCD share A and B panels in that XCD's L2.
+//
+// Epilogues (all fp32 with contraction off, then rounded like the eager chain):
+//   dequant : out = OUT( (float(acc) * s_tok[m]) * s_ch[n] )      (quant.py:162, 197)
+//   raw     : out = acc (int32 for INT8, fp32 for FP8)             (parity hook)
+//   swiglu  : weights interleaved in blocks of 32 rows [g0..g31, u0..u31, g32..];
+//             g = OUT(deq(gate)), u = OUT(deq(up)),
+//             h = OUT( OUT(g / (1 + exp(-g))) * u )                 (trtllm_stack.py:131-134)
+//             and row_amax[m] = max(row_amax[m], |h|) by atomic max.
+//   residual: out = OUT( float(res[m, n]) + OUT(deq(acc)) )         (core.py:215)
+#pragma once
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <type_traits>
+
+namespace d3 {
+
+
+constexpr int kBK = 128;  // bytes of K per pipeline step
+constexpr int kGroupM = 4;
+
+template <int MODE>
+struct Mfma;
+template <>
+struct Mfma<kInt8> {
+  typedef v4i frag;    // 16 bytes of K per lane, 32 K per instruction
+  typedef v16i acc;
+  static constexpr int kSub = kBK / 32;
+  __device__ static __forceinline__ acc run(frag a, frag b, acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<kFp8> {
+  typedef v8i frag;    // 32 bytes of K per lane, 64 K per instruction
+  typedef v16f acc;
+  static constexpr int kSub = kBK / 64;
+  __device__ static __forceinline__ acc run(frag a, frag b, acc c) {
+    // format 0 = FP8 E4M3 for both operands; E8M0 scale 127 = 1.0
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+  }
+};
+
+// 128-byte rows: a ds_read_b128 serves 16 lanes per cycle from 64 banks (256 B), i.e. two rows of 8
+// chunks; XOR-ing the chunk with (row >> 1) & 7 puts the 16 rows of one cycle on 16 distinct chunks.
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 1) & 7)) << 4); }
+
+// Map a linear workgroup id to (tile_m, tile_n): XCD-contiguous, then grouped.
+__device__ __forceinline__ void tile_of(int bid, int nb, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int full = nb >> 3, rem = nb & 7;
+  const int xcd = bid & 7, local = bid >> 3;
+  const int logical = xcd * full + (xcd < rem ? xcd : rem) + local;
+  const int per_group = kGroupM * tiles_n;
+  const int group = logical / per_group;
+  const int first_m = group * kGroupM;
+  const int gsz = min(tiles_m - first_m, kGroupM);
+  const int in_group = logical - group * per_group;
+  tm = first_m + in_group % gsz;
+  tn = in_group / gsz;
+}
+
+// Epilogue shared by the GEMM kernels. acc[i][j] is the 32x32 MFMA block at
+// rows wrow0 + 32 i, columns wcol0 + 32 j of the output; register r of lane l
+// holds row 8*(r/4) + 4*(l/32) + (r%4), column l%32 of its block.
+//
+// vmcnt counts loads and stores in issue order, so a load issued after stores
+// waits for them too: every token scale, row-map entry and channel scale the
+// tile needs is loaded before the first store (residuals per 32-row block).
+// FULL (the whole wave tile lies inside the output) drops every per-element
+// predicate, so the stores are straight-line code with no waits between them.
+template <int MODE, int TM, int TN, int EPI, int OUT, bool FULL, bool MAP, typename ACC>
+__device__ __forceinline__ void epilogue_impl(const GemmParams& p, ACC (&acc)[TM][TN], int64_t wrow0, int64_t wcol0,
+                                              int lane) {
+  const int64_t M = p.M, N = p.N;
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  const float* __restrict__ a_scale = p.a_scale;
+  const float* __restrict__ w_scale = p.w_scale;
+  const int32_t* __restrict__ row_map = p.row_map;
+  auto row_of = [&](int i, int r) -> int64_t { return wrow0 + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3); };
+
+  if constexpr (EPI == kEpiSwiGLU) {
+    float sg[TN / 2], su[TN / 2];
+    int64_t hcol[TN / 2];
+    bool cok[TN / 2];
+#pragma unroll
+    for (int jp = 0; jp < TN / 2; ++jp) {
+      const int64_t cg = wcol0 + (2 * jp) * 32 + lrow;  // interleaved gate column; its up column is cg + 32
+      cok[jp] = FULL || cg + 32 < N;
+      hcol[jp] = (cg >> 6) * 32 + (cg & 31);
+      sg[jp] = cok[jp] ? w_scale[cg] : 0.0f;
+      su[jp] = cok[jp] ? w_scale[cg + 32] : 0.0f;
+    }
+    // all token scales up front when the accumulators leave room (AGPR-resident tiles), else per block
+    constexpr bool kHoist = TM * TN * 16 > 128;
+    float st[kHoist ? TM : 1][16];
+    auto load_st = [&](int i, float* dst) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dst[r] = (FULL || row_of(i, r) < M) ? a_scale[row_of(i, r)] : 0.0f;
+    };
+    if constexpr (kHoist) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) load_st(i, st[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      if constexpr (!kHoist) load_st(i, st[0]);
+      float* sti = st[kHoist ? i : 0];
+      float rmax[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        rmax[r] = 0.0f;
+        const int64_t row = row_of(i, r);
+#pragma unroll
+        for (int jp = 0; jp < TN / 2; ++jp) {
+          if (FULL || (row < M && cok[jp])) {
+            float g = (float)acc[i][2 * jp][r];
+            g = g * sti[r];
+            g = round_to<OUT>(g * sg[jp]);
+            float u = (float)acc[i][2 * jp + 1][r];
+            u = u * sti[r];
+            u = round_to<OUT>(u * su[jp]);
+            const float e = expf(-g);
+            const float den = 1.0f + e;
+            const float sl = round_to<OUT>(g / den);
+            const float h = round_to<OUT>(sl * u);
+            store_elem<OUT>(p.out, row * p.ldo + hcol[jp], h);
+            rmax[r] = fmaxf(rmax[r], fabsf(h));
+          }
+        }
+      }
+      if (p.row_amax) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float v = rmax[r];
+#pragma unroll
+          for (int o = 1; o < 32; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+          const int64_t row = row_of(i, r);
+          if (lrow == 0 && (FULL || row < M)) atomicMax((unsigned int*)(p.row_amax + row), __float_as_uint(v));
+        }
+      }
+    }
+  } else {
+    float sc[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = wcol0 + j * 32 + lrow;
+      sc[j] = (EPI != kEpiRaw && (FULL || col < N)) ? w_scale[col] : 0.0f;
+    }
+    // all token scales / output rows up front when the accumulators leave room, else per block
+    constexpr bool kHoist = TM * TN * 16 > 128;
+    float st_[kHoist ? TM : 1][16];
+    int32_t orow_[kHoist ? TM : 1][16];
+    auto load_rows = [&](int i, float* st, int32_t* orow) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = row_of(i, r);
+        const bool ok = FULL || row < M;
+        if constexpr (MAP) orow[r] = ok ? row_map[row] : -1;
+        else orow[r] = ok ? (int32_t)row : -1;
+        st[r] = (EPI != kEpiRaw && ok) ? a_scale[row] : 0.0f;
+      }
+    };
+    if constexpr (kHoist) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) load_rows(i, st_[i], orow_[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      if constexpr (!kHoist) load_rows(i, st_[0], orow_[0]);
+      const float* st = st_[kHoist ? i : 0];
+      const int32_t* orow = orow_[kHoist ? i : 0];
+      float res[EPI == kEpiResidual ? 16 : 1][EPI == kEpiResidual ? TN : 1];
+      if constexpr (EPI == kEpiResidual) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const int64_t col = wcol0 + j * 32 + lrow;
+            res[r][j] = (FULL || (orow[r] >= 0 && col < N)) ? load_elem<OUT>(p.res, (int64_t)orow[r] * p.ldr + col)
+                                                              : 0.0f;
+          }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if (!FULL && orow[r] < 0) continue;
+        const int64_t obase = (int64_t)orow[r] * p.ldo;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int64_t col = wcol0 + j * 32 + lrow;
+          if (!FULL && col >= N) continue;
+          if constexpr (EPI == kEpiRaw) {
+            if constexpr (MODE == kInt8) ((int32_t*)p.out)[obase + col] = acc[i][j][r];
+            else ((float*)p.out)[obase + col] = acc[i][j][r];
+          } else {
+            float v = (float)acc[i][j][r];
+            v = v * st[r];
+            v = v * sc[j];
+            if constexpr (EPI == kEpiResidual) {
+              v = round_to<OUT>(v);
+              v = res[r][j] + v;
+            }
+            store_elem<OUT>(p.out, obase + col, v);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int MODE, int TM, int TN, int EPI, int OUT, typename ACC>
+__device__ __forceinline__ void epilogue(const GemmParams& p, ACC (&acc)[TM][TN], int64_t wrow0, int64_t wcol0,
+                                         int lane) {
+  const bool full = wrow0 + TM * 32 <= p.M && wcol0 + TN * 32 <= p.N;
+  if constexpr (EPI == kEpiSwiGLU) {
+    if (full) epilogue_impl<MODE, TM, TN, EPI, OUT, true, false>(p, acc, wrow0, wcol0, lane);
+    else epilogue_impl<MODE, TM, TN, EPI, OUT, false, false>(p, acc, wrow0, wcol0, lane);
+  } else if (p.row_map) {
+    if (full) epilogue_impl<MODE, TM, TN, EPI, OUT, true, true>(p, acc, wrow0, wcol0, lane);
+    else epilogue_impl<MODE, TM, TN, EPI, OUT, false, true>(p, acc, wrow0, wcol0, lane);
+  } else {
+    if (full) epilogue_impl<MODE, TM, TN, EPI, OUT, true, false>(p, acc, wrow0, wcol0, lane);
+    else epilogue_impl<MODE, TM, TN, EPI, OUT, false, false>(p, acc, wrow0, wcol0, lane);
+  }
+}
+
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
+__global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8(GemmParams p) {
+  using MF = Mfma<MODE>;
+  typedef typename MF::frag frag_t;
+  typedef typename MF::acc acc_t;
+  constexpr int NT = WM * WN * 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int A_LD = BM * 8 / NT, B_LD = BN * 8 / NT;
+  constexpr int STAGE = (BM + BN) * kBK;
+  static_assert(TM >= 1 && TN >= 1 && A_LD >= 1 && B_LD >= 1, "tile config");
+  static_assert(EPI != kEpiSwiGLU || (TN % 2 == 0), "swiglu needs gate/up block pairs");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  int tm, tn;
+  tile_of(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t M = p.M, N = p.N, K = p.K;
+
+  v4i ra[A_LD], rb[B_LD];
+  auto gload = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int id = i * NT + tid, row = id >> 3, ch = id & 7;
+      const int64_t gm = m0 + row, kk = k0 + ch * 16;
+      ra[i] = (gm < M && kk < K) ? *(const v4i*)(p.a + gm * p.lda + kk) : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int id = i * NT + tid, row = id >> 3, ch = id & 7;
+      const int64_t gn = n0 + row, kk = k0 + ch * 16;
+      rb[i] = (gn < N && kk < K) ? *(const v4i*)(p.w + gn * p.ldw + kk) : v4i{0, 0, 0, 0};
+    }
+  };
+  auto swrite = [&](int buf) {
+    uint8_t* sa = lds + buf * STAGE;
+    uint8_t* sb = sa + BM * kBK;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int id = i * NT + tid, row = id >> 3, ch = id & 7;
+      *(v4i*)(sa + lds_off(row, ch)) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int id = i * NT + tid, row = id >> 3, ch = id & 7;
+      *(v4i*)(sb + lds_off(row, ch)) = rb[i];
+    }
+  };
+
+  acc_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int nk = (int)((K + kBK - 1) / kBK);
+  gload(0);
+  swrite(0);
+  __syncthreads();
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((int64_t)(kt + 1) * kBK);
+    const uint8_t* sa = lds + buf * STAGE;
+    const uint8_t* sb = sa + BM * kBK;
+#pragma unroll
+    for (int s = 0; s < MF::kSub; ++s) {
+      frag_t af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * WTM + i * 32 + lrow;
+        if constexpr (MODE == kInt8) {
+          af[i] = *(const v4i*)(sa + lds_off(row, 2 * s + lhalf));
+        } else {
+          const v4i lo = *(const v4i*)(sa + lds_off(row, 4 * s + 2 * lhalf));
+          const v4i hi = *(const v4i*)(sa + lds_off(row, 4 * s + 2 * lhalf + 1));
+          af[i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int row = wn * WTN + j * 32 + lrow;
+        if constexpr (MODE == kInt8) {
+          bf[j] = *(const v4i*)(sb + lds_off(row, 2 * s + lhalf));
+        } else {
+          const v4i lo = *(const v4i*)(sb + lds_off(row, 4 * s + 2 * lhalf));
+          const v4i hi = *(const v4i*)(sb + lds_off(row, 4 * s + 2 * lhalf + 1));
+          bf[j] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = MF::run(af[i], bf[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) swrite(buf ^ 1);
+    __syncthreads();
+  }
+
+  epilogue<MODE, TM, TN, EPI, OUT>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane);
+}
+
+
+// ---------------------------------------------------------------------------
+// Pipelined kernel (K % 64 == 0): 64-byte K steps, 4 LDS stages filled by
+// direct global->LDS DMA (global_load_lds_dwordx4), one barrier per step.
+//
+//   * DMA: each instruction of a wave writes 1 KiB of LDS (64 lanes x 16 B):
+//     16 rows of 64 bytes. Lane j carries row r0 + j/4 and physical chunk
+//     j%4, i.e. logical K chunk (j%4) ^ ((row >> 2) & 3): the XOR swizzle that
+//     makes the MFMA operand reads (one 16-byte chunk of 32 consecutive rows)
+//     conflict-free (a ds_read_b128 serves 16 lanes per cycle from 64 banks).
+//     Sources are a uniform base (SGPRs, advanced by 64 bytes per step) plus
+//     a 32-bit per-lane offset; the LDS address is this wave's slot in stage
+//     0 plus a compile-time stage/row offset. Rows past M (or N) are clamped
+//     to the last row: they only feed output rows (columns) never stored.
+//   * Operands: A fragments are single-buffered (the fragment for the next
+//     step is read right after its last MFMA of this step); B fragments are
+//     double-buffered by step parity.
+//   * Step kt (stage U = kt % 4 holds its operands): PRE MFMAs; wait for this
+//     wave's LDS reads and for its DMA of step kt+1; barrier (so every wave's
+//     DMA of step kt+1 has landed and every wave is done reading stage U);
+//     then the remaining MFMAs, each followed by its share of the next step's
+//     fragment reads (stage U+1) and of the DMA of step kt+4 (into stage U).
+//     sched_barrier after every slot keeps that interleave: the matrix pipe
+//     always has queued work while LDS and DMA requests issue.
+//   * Steps with a full pipeline ahead run unchecked; the last steps of the
+//     K loop (CHECKED) guard the reads and DMAs that would pass the end.
+// ---------------------------------------------------------------------------
+constexpr int kBK2 = 64;
+constexpr int kStages = 4;
+
+// 64-byte rows: the 16 lanes of one ds_read_b128 cycle read rows r..r+15 (four rows per 256-byte bank
+// line); XOR-ing the chunk with (row >> 2) & 3 spreads them over the 16 bank groups.
+__device__ __forceinline__ int lds_off64(int row, int chunk) { return row * kBK2 + ((chunk ^ ((row >> 2) & 3)) << 4); }
+
+// s_barrier without the fence __syncthreads() adds (whose vmcnt(0) would drain
+// the DMA pipeline); the empty asm keeps the compiler from moving LDS accesses
+// across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Calls f(std::integral_constant<int, I>) for I in [B, E), in order.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // s_waitcnt encoding (gfx9): vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+#define D3_LDS_PTR(p) ((__attribute__((address_space(3))) const void*)(p))
+
+// One wave-wide 16-byte-per-lane DMA: lane l's 16 bytes at gbase + voff land
+// at LDS lds_base + OFF + 16 l. Issued as inline asm so the compiler does not
+// model the LDS write (it would otherwise insert vmcnt(0) before LDS reads it
+// cannot prove disjoint, draining the pipeline); every wait on this DMA is
+// explicit (wait_vmcnt + barrier). M0 holds the LDS address; the s_nop covers
+// the M0-write -> LDS-DMA hazard.
+template <int OFF>
+__device__ __forceinline__ void dma16(const uint8_t* gbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile(
+      "s_add_u32 m0, %1, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %3"
+      :
+      : "v"(voff), "s"(lds_base), "i"(OFF), "s"(gbase)
+      : "memory", "m0", "scc");
+}
+
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
+__global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
+  using MF = Mfma<MODE>;
+  typedef typename MF::frag frag_t;
+  typedef typename MF::acc acc_t;
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int A_BYTES = BM * kBK2, B_BYTES = BN * kBK2, STAGE = A_BYTES + B_BYTES;
+  constexpr int A_DMA = A_BYTES / (1024 * NW), B_DMA = B_BYTES / (1024 * NW);
+  constexpr int DPS = A_DMA + B_DMA;            // DMA instructions per wave per step
+  constexpr int SUB = MODE == kInt8 ? 2 : 1;    // MFMAs along K per 64-byte step
+  constexpr int FW = MODE == kInt8 ? 1 : 2;     // 16-byte LDS words per MFMA operand
+  constexpr int NMF = SUB * TM * TN;            // MFMAs per step
+  constexpr int PRE = NMF >= 4 ? 2 : 1;         // MFMAs issued before the barrier
+  constexpr int SLOTS = NMF - PRE;
+  constexpr int NBW = SUB * TN * FW;            // B words read per step
+  static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "DMA split");
+  static_assert(EPI != kEpiSwiGLU || (TN % 2 == 0), "swiglu needs gate/up block pairs");
+  static_assert(SLOTS >= 1, "tile too small for the interleave");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  int tm, tn;
+  tile_of(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int nk = (int)(p.K / kBK2);
+  const int lrow = lane & 31, lhalf = lane >> 5;
+
+  // DMA sources: uniform tile bases + per-lane 32-bit offsets (the host keeps every operand
+  // offset below 2^32 for this kernel)
+  const uint8_t* a_base = p.a + m0 * p.lda;
+  const uint8_t* b_base = p.w + n0 * p.ldw;
+  uint32_t a_off[A_DMA], b_off[B_DMA];
+#pragma unroll
+  for (int i = 0; i < A_DMA; ++i) {
+    const int row = (i * NW + wave) * 16 + (lane >> 2);
+    const int ch = (lane & 3) ^ ((row >> 2) & 3);
+    a_off[i] = (uint32_t)((min(m0 + row, p.M - 1) - m0) * p.lda + ch * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < B_DMA; ++i) {
+    const int row = (i * NW + wave) * 16 + (lane >> 2);
+    const int ch = (lane & 3) ^ ((row >> 2) & 3);
+    b_off[i] = (uint32_t)((min(n0 + row, p.N - 1) - n0) * p.ldw + ch * 16);
+  }
+  const uint32_t lds_wave =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)D3_LDS_PTR(lds) + (uint32_t)wave * 1024u);
+
+  // DMA d of step kt into stage U
+  auto dma_one = [&](auto u_c, auto d_c, int kt) {
+    constexpr int U = decltype(u_c)::value % kStages, d = decltype(d_c)::value;
+    const int64_t kb = (int64_t)kt * kBK2;
+    if constexpr (d < A_DMA) dma16<U * STAGE + d * NW * 1024>(a_base + kb, a_off[d], lds_wave);
+    else dma16<U * STAGE + A_BYTES + (d - A_DMA) * NW * 1024>(b_base + kb, b_off[d - A_DMA], lds_wave);
+  };
+  auto dma_stage = [&](auto u_c, int kt) { static_for<0, DPS>([&](auto d_c) { dma_one(u_c, d_c, kt); }); };
+
+  acc_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  frag_t fa[SUB][TM];     // A operands of the current step (single buffer)
+  frag_t fb[2][SUB][TN];  // B operands, by step parity
+
+  // A word (s, i, h) / B word w of stage U (h: 16-byte half of an FP8 operand)
+  auto read_a = [&](auto u_c, auto s_c, auto i_c, auto h_c) {
+    constexpr int U = decltype(u_c)::value % kStages, s = decltype(s_c)::value;
+    constexpr int i = decltype(i_c)::value, h = decltype(h_c)::value;
+    const int chunk = MODE == kInt8 ? 2 * s + lhalf : 2 * lhalf + h;
+    const v4i v = *(const v4i*)(lds + U * STAGE + lds_off64(wm * WTM + i * 32 + lrow, chunk));
+    if constexpr (MODE == kInt8) fa[s][i] = v;
+    else if constexpr (h == 0) fa[s][i].lo = v;
+    else fa[s][i].hi = v;
+  };
+  auto read_b = [&](auto u_c, auto p_c, auto w_c) {
+    constexpr int U = decltype(u_c)::value % kStages, P = decltype(p_c)::value, w = decltype(w_c)::value;
+    constexpr int s = w / (TN * FW), j = (w / FW) % TN, h = w % FW;
+    const int chunk = MODE == kInt8 ? 2 * s + lhalf : 2 * lhalf + h;
+    const v4i v = *(const v4i*)(lds + U * STAGE + A_BYTES + lds_off64(wn * WTN + j * 32 + lrow, chunk));
+    if constexpr (MODE == kInt8) fb[P][s][j] = v;
+    else if constexpr (h == 0) fb[P][s][j].lo = v;
+    else fb[P][s][j].hi = v;
+  };
+  // all operands of one step (prologue)
+  auto read_all = [&](auto u_c, auto p_c) {
+    static_for<0, SUB>([&](auto s_c) {
+      static_for<0, TM>([&](auto i_c) {
+        static_for<0, FW>([&](auto h_c) { read_a(u_c, s_c, i_c, h_c); });
+      });
+    });
+    static_for<0, NBW>([&](auto w_c) { read_b(u_c, p_c, w_c); });
+  };
+  auto mfma_q = [&](auto p_c, auto q_c) {
+    constexpr int P = decltype(p_c)::value, q = decltype(q_c)::value;
+    constexpr int s = q / (TM * TN), i = (q / TN) % TM, j = q % TN;
+    acc[i][j] = MF::run(fa[s][i], fb[P][s][j], acc[i][j]);
+  };
+
+  // Step kt with operands in stage U = kt % 4 and B parity P = kt & 1.
+  auto step = [&](auto u_c, auto chk_c, int kt) {
+    constexpr int U = decltype(u_c)::value;
+    constexpr int P = U & 1;
+    constexpr bool CHECKED = decltype(chk_c)::value;
+    static_for<0, PRE>([&](auto q_c) { mfma_q(std::integral_constant<int, P>{}, q_c); });
+    __builtin_amdgcn_sched_barrier(0);
+    const bool rd = !CHECKED || kt + 1 < nk;
+    const bool fetch = !CHECKED || kt + kStages < nk;
+    wait_lgkm0();
+    if constexpr (!CHECKED) {
+      wait_vmcnt<2 * DPS>();
+    } else {
+      const int after = min(kStages - 2, nk - 2 - kt);  // DMA steps issued after step kt+1
+      if (after >= 2) wait_vmcnt<2 * DPS>();
+      else if (after == 1) wait_vmcnt<DPS>();
+      else wait_vmcnt<0>();
+    }
+    lds_barrier();
+    static_for<PRE, NMF>([&](auto q_c) {
+      constexpr int q = decltype(q_c)::value, k = q - PRE;
+      mfma_q(std::integral_constant<int, P>{}, q_c);
+      // B words of the next step in this slot's share
+      static_for<k * NBW / SLOTS, (k + 1) * NBW / SLOTS>([&](auto w_c) {
+        if (rd) read_b(std::integral_constant<int, U + 1>{}, std::integral_constant<int, P ^ 1>{}, w_c);
+      });
+      // A operand (s, i) of the next step once its last MFMA of this step has issued
+      static_for<0, SUB * TM>([&](auto a_c) {
+        constexpr int s = decltype(a_c)::value / TM, i = decltype(a_c)::value % TM;
+        constexpr int last = s * TM * TN + i * TN + TN - 1;
+        if constexpr ((last < PRE ? PRE : last) == q) {
+          static_for<0, FW>([&](auto h_c) {
+            if (rd) read_a(std::integral_constant<int, U + 1>{}, std::integral_constant<int, s>{},
+                           std::integral_constant<int, i>{}, h_c);
+          });
+        }
+      });
+      // DMA of step kt+4 into stage U, in this slot's share
+      static_for<k * DPS / SLOTS, (k + 1) * DPS / SLOTS>([&](auto d_c) {
+        if (fetch) dma_one(u_c, d_c, kt + kStages);
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // Prologue: DMA of steps 0..3 fills every stage; then the operands of step 0.
+  dma_stage(std::integral_constant<int, 0>{}, 0);
+  if (nk > 1) dma_stage(std::integral_constant<int, 1>{}, 1);
+  if (nk > 2) dma_stage(std::integral_constant<int, 2>{}, 2);
+  if (nk > 3) dma_stage(std::integral_constant<int, 3>{}, 3);
+  {
+    const int after = min(kStages - 1, nk - 1);  // DMA steps issued after step 0
+    if (after >= 3) wait_vmcnt<3 * DPS>();
+    else if (after == 2) wait_vmcnt<2 * DPS>();
+    else if (after == 1) wait_vmcnt<DPS>();
+    else wait_vmcnt<0>();
+  }
+  lds_barrier();
+  read_all(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+
+  using Steady = std::integral_constant<bool, false>;
+  using Checked = std::integral_constant<bool, true>;
+  int kt0 = 0;
+  for (; kt0 + 2 * kStages <= nk; kt0 += 4) {
+    step(std::integral_constant<int, 0>{}, Steady{}, kt0);
+    step(std::integral_constant<int, 1>{}, Steady{}, kt0 + 1);
+    step(std::integral_constant<int, 2>{}, Steady{}, kt0 + 2);
+    step(std::integral_constant<int, 3>{}, Steady{}, kt0 + 3);
+  }
+  for (; kt0 < nk; kt0 += 4) {
+    step(std::integral_constant<int, 0>{}, Checked{}, kt0);
+    if (kt0 + 1 < nk) step(std::integral_constant<int, 1>{}, Checked{}, kt0 + 1);
+    if (kt0 + 2 < nk) step(std::integral_constant<int, 2>{}, Checked{}, kt0 + 2);
+    if (kt0 + 3 < nk) step(std::integral_constant<int, 3>{}, Checked{}, kt0 + 3);
+  }
+
+  epilogue<MODE, TM, TN, EPI, OUT>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane);
+}
+
+// ---------------------------------------------------------------------------
+// host side: tile-config selection and dispatch
+// ---------------------------------------------------------------------------
+enum TileCfg : int {
+  kTileAuto = -1,
+  kTile256 = 0,      // register-staged 256x256, 4 waves
+  kTile128 = 1,      // register-staged 128x128, 4 waves
+  kTile64x128 = 2,   // register-staged 64x128, 4 waves
+  kDma256w8 = 3,     // DMA pipeline 256x256, 8 waves (128x64 each), 4 stages
+  kDma256w4 = 4,     // DMA pipeline 256x256, 4 waves (128x128 each), 4 stages
+  kDma128w4 = 5,     // DMA pipeline 128x128, 4 waves (64x64 each), 4 stages
+  kDma256x128w4 = 6, // DMA pipeline 256x128, 4 waves (128x64 each), 4 stages
+  kTileCount = 7
+};
+
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
+static hipError_t launch_cfg(GemmParams p, hipStream_t st) {
+  p.tiles_m = (int)((p.M + BM - 1) / BM);
+  p.tiles_n = (int)((p.N + BN - 1) / BN);
+  const int64_t nb = (int64_t)p.tiles_m * p.tiles_n;
+  hipLaunchKernelGGL((gemm_w8a8<MODE, BM, BN, WM, WN, EPI, OUT>), dim3((unsigned)nb), dim3(WM * WN * 64), 0, st, p);
+  return hipGetLastError();
+}
+
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
+static hipError_t launch_dma(GemmParams p, hipStream_t st) {
+  p.tiles_m = (int)((p.M + BM - 1) / BM);
+  p.tiles_n = (int)((p.N + BN - 1) / BN);
+  const int64_t nb = (int64_t)p.tiles_m * p.tiles_n;
+  hipLaunchKernelGGL((gemm_w8a8_dma<MODE, BM, BN, WM, WN, EPI, OUT>), dim3((unsigned)nb), dim3(WM * WN * 64), 0,
+                     st, p);
+  return hipGetLastError();
+}
+
+static int choose_tile(int64_t M, int64_t N, int64_t K) {
+  const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  if (K % kBK2 == 0) {
+    if (t256 >= 256) return kDma256w8;
+    if (t128 >= 192) return kDma128w4;
+    return kTile64x128;
+  }
+  if (t256 >= 256) return kTile256;
+  if (t128 >= 192) return kTile128;
+  return kTile64x128;
+}
+
+// The DMA kernels address operands as a tile base plus a 32-bit per-lane offset.
+static bool dma_offsets_fit(const GemmParams& p) {
+  const int64_t lim = (int64_t)1 << 32;
+  return (p.M - 1) * p.lda + p.K < lim && (p.N - 1) * p.ldw + p.K < lim;
+}
+
+template <int MODE, int EPI, int OUT>
+hipError_t launch_epi(GemmParams p, int tile, hipStream_t st) {
+  if (tile == kTileAuto) {
+    tile = choose_tile(p.M, p.N, p.K);
+    if (tile >= kDma256w8 && !dma_offsets_fit(p)) tile = tile == kDma256w8 ? kTile256 : kTile128;
+  }
+  if (tile >= kDma256w8 && (p.K % kBK2 != 0 || !dma_offsets_fit(p))) return hipErrorInvalidValue;
+  switch (tile) {
+    case kTile256: return launch_cfg<MODE, 256, 256, 2, 2, EPI, OUT>(p, st);
+    case kTile128: return launch_cfg<MODE, 128, 128, 2, 2, EPI, OUT>(p, st);
+    case kTile64x128: return launch_cfg<MODE, 64, 128, 2, 2, EPI, OUT>(p, st);
+    case kDma256w8: return launch_dma<MODE, 256, 256, 2, 4, EPI, OUT>(p, st);
+    case kDma256w4: return launch_dma<MODE, 256, 256, 2, 2, EPI, OUT>(p, st);
+    case kDma128w4: return launch_dma<MODE, 128, 128, 2, 2, EPI, OUT>(p, st);
+    case kDma256x128w4: return launch_dma<MODE, 256, 128, 2, 2, EPI, OUT>(p, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace d3

@@ -16,30 +16,69 @@ namespace d3 {
 
 constexpr int kQuantWaves = 4;  // rows per 256-thread block
 
-// 8 consecutive elements of dtype DT at p (16B-aligned for 16-bit types,
-// 32B-aligned for fp32) -> 8 floats.
-template <int DT>
-__device__ __forceinline__ void load8(const void* p, float* v) {
-  if constexpr (DT == kF32) {
-    const float4* q = (const float4*)p;
-    float4 a = q[0], b = q[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  } else {
-    uint4 u = *(const uint4*)p;
-    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+// One row of a [*, K] tensor held by one wave: lane l owns the 8-element
+// chunks at columns 512 c + 8 l (c < NCH), kept as raw 16-byte words (32 for
+// fp32) so that a row of 16-bit values costs 4 VGPRs per chunk.
+//
+// load() issues every chunk's load before any is consumed: a chunk past the
+// end of the row reads the row's last 8 elements instead (K % 8 == 0 and
+// K >= 8, so the address is always inside the row) and is masked by valid().
+// Putting the loads under `if (col < K)` instead makes the compiler wait for
+// each load before issuing the next, serializing NCH HBM round trips.
+template <int DT, int NCH>
+struct RowChunks {
+  static constexpr int kWords = DT == kF32 ? 2 : 1;
+  static constexpr int kES = DT == kF32 ? 4 : 2;
+  uint4 raw[NCH][kWords];
+
+  __device__ __forceinline__ static int64_t col(int c, int lane) { return (int64_t)c * 512 + lane * 8; }
+  __device__ __forceinline__ static bool valid(int c, int lane, int64_t K) { return col(c, lane) < K; }
+
+  __device__ __forceinline__ void load(const char* row, int64_t K, int lane) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (DT == kBF16) {
-        v[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu);
-        v[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
-      } else {
-        v[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
-        v[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+    for (int c = 0; c < NCH; ++c) {
+      const int64_t cc = min(col(c, lane), K - 8);
+      const uint4* src = (const uint4*)(row + cc * kES);
+#pragma unroll
+      for (int w = 0; w < kWords; ++w) raw[c][w] = src[w];
+    }
+  }
+  __device__ __forceinline__ void get(int c, float* v) const {
+    if constexpr (DT == kF32) {
+      const uint4 a = raw[c][0], b = raw[c][1];
+      v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+      v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y); v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
+    } else {
+      const uint4 u = raw[c][0];
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (DT == kBF16) {
+          v[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu);
+          v[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
+        } else {
+          v[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+          v[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+        }
       }
     }
   }
-}
+
+  // max |x| over the valid chunks
+  __device__ __forceinline__ float amax(int64_t K, int lane) const {
+    float m = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (valid(c, lane, K)) {
+        float v[8];
+        get(c, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+      }
+    }
+    return m;
+  }
+};
 
 template <int DT>
 __device__ __forceinline__ void store8(void* p, const float* v) {
@@ -96,26 +135,18 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ x
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
   if (row >= M) return;
-  constexpr int ES = DT == kF32 ? 4 : 2;
-  const char* xr = (const char*)x + row * ldx * ES;
-  float v[NCH][8];
-  float amax = 0.0f;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int64_t col = (int64_t)c * 512 + lane * 8;
-    if (col < K) {
-      load8<DT>(xr + col * ES, v[c]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
-    }
-  }
-  amax = wave_max(amax);
-  const float s = scale_from_amax<MODE>(amax);
+  using RC = RowChunks<DT, NCH>;
+  RC x_;
+  x_.load((const char*)x + row * ldx * RC::kES, K, lane);
+  const float s = scale_from_amax<MODE>(wave_max(x_.amax(K, lane)));
   char* qr = (char*)q + row * ldq;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int64_t col = (int64_t)c * 512 + lane * 8;
-    if (col < K) quant_store8<MODE>(qr + col, v[c], s);
+    if (RC::valid(c, lane, K)) {
+      float v[8];
+      x_.get(c, v);
+      quant_store8<MODE>(qr + RC::col(c, lane), v, s);
+    }
   }
   if (lane == 0) scale[row] = s;
 }
@@ -153,17 +184,17 @@ __global__ __launch_bounds__(256) void quant_rows_amax_vec(const void* __restric
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
   if (row >= M) return;
-  constexpr int ES = DT == kF32 ? 4 : 2;
+  using RC = RowChunks<DT, NCH>;
+  RC h_;
+  h_.load((const char*)h + row * ldh * RC::kES, K, lane);
   const float s = scale_from_amax<MODE>(amax_in[row]);
-  const char* hr = (const char*)h + row * ldh * ES;
   char* qr = (char*)q + row * ldq;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int64_t col = (int64_t)c * 512 + lane * 8;
-    if (col < K) {
+    if (RC::valid(c, lane, K)) {
       float v[8];
-      load8<DT>(hr + col * ES, v);
-      quant_store8<MODE>(qr + col, v, s);
+      h_.get(c, v);
+      quant_store8<MODE>(qr + RC::col(c, lane), v, s);
     }
   }
   if (lane == 0) scale[row] = s;
@@ -184,19 +215,21 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
   if (row >= M) return;
-  constexpr int ES = DT == kF32 ? 4 : 2;
-  constexpr int ESW = DTW == kF32 ? 4 : 2;
-  const char* xr = (const char*)x + row * ldx * ES;
-  float v[NCH][8];
+  using RC = RowChunks<DT, NCH>;
+  using RW = RowChunks<DTW, NCH>;
+  RC x_;
+  x_.load((const char*)x + row * ldx * RC::kES, K, lane);
+  RW w_;
+  w_.load((const char*)w, K, lane);
   float ss = 0.0f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int64_t col = (int64_t)c * 512 + lane * 8;
-    if (col < K) {
-      load8<DT>(xr + col * ES, v[c]);
+    if (RC::valid(c, lane, K)) {
+      float v[8];
+      x_.get(c, v);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float sq = v[c][i] * v[c][i];
+        const float sq = v[i] * v[i];
         ss = ss + sq;
       }
     }
@@ -205,33 +238,32 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
   const float var = ss / (float)K;
   const float t = var + eps;
   const float rstd = (float)(1.0 / sqrt((double)t));
+  float y[NCH][8];
   float amax = 0.0f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int64_t col = (int64_t)c * 512 + lane * 8;
-    if (col < K) {
-      float g[8];
-      load8<DTW>((const char*)w + col * ESW, g);
+    if (RC::valid(c, lane, K)) {
+      float v[8], g[8];
+      x_.get(c, v);
+      w_.get(c, g);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float gain = zero_centered ? (1.0f + g[i]) : g[i];
-        const float nx = v[c][i] * rstd;
-        const float y = round_to<DT>(nx * gain);
-        v[c][i] = y;
-        amax = fmaxf(amax, fabsf(y));
+        const float nx = v[i] * rstd;
+        y[c][i] = round_to<DT>(nx * gain);
+        amax = fmaxf(amax, fabsf(y[c][i]));
       }
     }
   }
-  amax = wave_max(amax);
-  const float s = scale_from_amax<MODE>(amax);
+  const float s = scale_from_amax<MODE>(wave_max(amax));
   char* qr = (char*)q + row * ldq;
-  char* nr = normed ? (char*)normed + row * ldn * ES : nullptr;
+  char* nr = normed ? (char*)normed + row * ldn * RC::kES : nullptr;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int64_t col = (int64_t)c * 512 + lane * 8;
-    if (col < K) {
-      quant_store8<MODE>(qr + col, v[c], s);
-      if (nr) store8<DT>(nr + col * ES, v[c]);
+    if (RC::valid(c, lane, K)) {
+      const int64_t col = RC::col(c, lane);
+      quant_store8<MODE>(qr + col, y[c], s);
+      if (nr) store8<DT>(nr + col * RC::kES, y[c]);
     }
   }
   if (lane == 0) {
@@ -273,26 +305,18 @@ __global__ __launch_bounds__(256) void quant_rows_ragged_vec(
     return;
   }
   const int64_t dst = part + t;
-  constexpr int ES = DT == kF32 ? 4 : 2;
-  const char* xr = (const char*)x + prow * ldx * ES;
-  float v[NCH][8];
-  float amax = 0.0f;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int64_t col = (int64_t)c * 512 + lane * 8;
-    if (col < K) {
-      load8<DT>(xr + col * ES, v[c]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
-    }
-  }
-  amax = wave_max(amax);
-  const float s = scale_from_amax<MODE>(amax);
+  using RC = RowChunks<DT, NCH>;
+  RC x_;
+  x_.load((const char*)x + prow * ldx * RC::kES, K, lane);
+  const float s = scale_from_amax<MODE>(wave_max(x_.amax(K, lane)));
   char* qr = (char*)q + dst * ldq;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int64_t col = (int64_t)c * 512 + lane * 8;
-    if (col < K) quant_store8<MODE>(qr + col, v[c], s);
+    if (RC::valid(c, lane, K)) {
+      float v[8];
+      x_.get(c, v);
+      quant_store8<MODE>(qr + RC::col(c, lane), v, s);
+    }
   }
   if (lane == 0) {
     scale[dst] = s;

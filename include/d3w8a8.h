@@ -48,7 +48,8 @@ extern "C" {
 
 /* GEMM tile configurations (D3W8A8_TILE_AUTO picks one from M, N and K).
  * REG tiles stage K through registers and accept any K % 16 == 0; DMA tiles
- * use the direct global->LDS pipeline and need K % 64 == 0. */
+ * use the direct global->LDS pipeline and need K % 64 == 0 and each operand
+ * within 4 GiB of its first row ((rows - 1) * ld + K < 2^32). */
 #define D3W8A8_TILE_AUTO (-1)
 #define D3W8A8_TILE_256 0           /* REG 256x256, 4 waves */
 #define D3W8A8_TILE_128 1           /* REG 128x128, 4 waves */
