@@ -153,6 +153,10 @@ int d3w8a8_gemm(int mode, const void* a, int64_t lda, const float* a_scale, cons
   p.M = M; p.N = N; p.K = K;
   p.out = out; p.ldo = ldo; p.res = res; p.ldr = ldr;
   p.row_amax = row_amax; p.row_map = row_map;
+  const int oes = epilogue == D3W8A8_EPI_RAW ? 4 : esize(out_dtype);
+  // full tiles store 16-byte row chunks: rows of out (and res) must be 16-byte aligned
+  p.vec = (ldo * oes) % 16 == 0 && aligned(out, 16) && (epilogue == D3W8A8_EPI_RAW || aligned(w_scale, 16)) &&
+          (epilogue != D3W8A8_EPI_RESIDUAL || ((ldr * oes) % 16 == 0 && aligned(res, 16)));
   return hip_status(d3::launch_gemm(mode, p, epilogue, out_dtype, tile, (hipStream_t)stream), "gemm");
 }
 

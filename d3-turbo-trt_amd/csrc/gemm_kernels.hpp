@@ -17,9 +17,10 @@
 //     MFMA blocks: v_mfma_i32_32x32x32_i8 (INT8) or
 //     v_mfma_scale_f32_32x32x64_f8f6f4 with format E4M3 and unit scales (FP8).
 //     Operand lane l carries row (l & 31) and the K chunk selected by l >> 5;
-//     A and B use the same K assignment, so the dot product is complete.
-//   * Result lane layout (32x32 blocks): register r of lane l is
-//     row 8*(r/4) + 4*(l/32) + (r%4), column l%32.
+//     both operands use the same K assignment, so the dot product is complete.
+//     The weights are the MFMA's first operand and the activations its
+//     second, so each 32x32 result block is transposed: register r of lane l
+//     holds output row l%32, column 8*(r/4) + 4*(l/32) + (r%4).
 //   * Workgroups are remapped so that each XCD (the hardware deals
 //     workgroups round-robin over 8 XCDs) receives a contiguous run of tiles,
 //     ordered in groups of GROUP_M tile-rows, so concurrently running tiles on
@@ -86,167 +87,262 @@ __device__ __forceinline__ void tile_of(int bid, int nb, int tiles_m, int tiles_
   tn = in_group / gsz;
 }
 
-// Epilogue shared by the GEMM kernels. acc[i][j] is the 32x32 MFMA block at
-// rows wrow0 + 32 i, columns wcol0 + 32 j of the output; register r of lane l
-// holds row 8*(r/4) + 4*(l/32) + (r%4), column l%32 of its block.
-//
-// vmcnt counts loads and stores in issue order, so a load issued after stores
-// waits for them too: every token scale, row-map entry and channel scale the
-// tile needs is loaded before the first store (residuals per 32-row block).
-// FULL (the whole wave tile lies inside the output) drops every per-element
-// predicate, so the stores are straight-line code with no waits between them.
-template <int MODE, int TM, int TN, int EPI, int OUT, bool FULL, bool MAP, typename ACC>
-__device__ __forceinline__ void epilogue_impl(const GemmParams& p, ACC (&acc)[TM][TN], int64_t wrow0, int64_t wcol0,
+// Epilogue shared by the GEMM kernels. The MFMAs take the weights as their
+// first operand and the activations as their second, so acc[i][j] is the
+// transposed 32x32 output block: lane l holds output row
+//   wrow0 + 32 i + (l & 31)
+// and, in register 4 g + c (g, c in 0..3), output column
+//   wcol0 + 32 j + 8 g + 4 (l >> 5) + c.
+// Every lane therefore owns runs of 4 consecutive columns of one row: one
+// token scale per block row and float4 channel scales.
+
+// Edge tiles (partly outside the output, or outputs without 16-byte row
+// alignment): every element is checked and stored on its own, with its
+// scales loaded where they are used. Correct for any shape; the full-tile
+// path below carries the throughput.
+template <int MODE, int TM, int TN, int EPI, int OUT, bool MAP, typename ACC>
+__device__ __forceinline__ void epilogue_edge(const GemmParams& p, ACC (&acc)[TM][TN], int64_t wrow0, int64_t wcol0,
                                               int lane) {
   const int64_t M = p.M, N = p.N;
   const int lrow = lane & 31, lhalf = lane >> 5;
-  const float* __restrict__ a_scale = p.a_scale;
-  const float* __restrict__ w_scale = p.w_scale;
-  const int32_t* __restrict__ row_map = p.row_map;
-  auto row_of = [&](int i, int r) -> int64_t { return wrow0 + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3); };
-
-  if constexpr (EPI == kEpiSwiGLU) {
-    float sg[TN / 2], su[TN / 2];
-    int64_t hcol[TN / 2];
-    bool cok[TN / 2];
 #pragma unroll
-    for (int jp = 0; jp < TN / 2; ++jp) {
-      const int64_t cg = wcol0 + (2 * jp) * 32 + lrow;  // interleaved gate column; its up column is cg + 32
-      cok[jp] = FULL || cg + 32 < N;
-      hcol[jp] = (cg >> 6) * 32 + (cg & 31);
-      sg[jp] = cok[jp] ? w_scale[cg] : 0.0f;
-      su[jp] = cok[jp] ? w_scale[cg + 32] : 0.0f;
-    }
-    // all token scales up front when the accumulators leave room (AGPR-resident tiles), else per block
-    constexpr bool kHoist = TM * TN * 16 > 128;
-    float st[kHoist ? TM : 1][16];
-    auto load_st = [&](int i, float* dst) {
+  for (int i = 0; i < TM; ++i) {
+    const int64_t row = wrow0 + i * 32 + lrow;
+    const bool rok = row < M;
+    const float st = (EPI != kEpiRaw && rok) ? p.a_scale[row] : 0.0f;
+    const int64_t orow = MAP ? (rok ? (int64_t)p.row_map[row] : 0) : row;
+    if constexpr (EPI == kEpiSwiGLU) {
+      float rmax = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dst[r] = (FULL || row_of(i, r) < M) ? a_scale[row_of(i, r)] : 0.0f;
-    };
-    if constexpr (kHoist) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i) load_st(i, st[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      if constexpr (!kHoist) load_st(i, st[0]);
-      float* sti = st[kHoist ? i : 0];
-      float rmax[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        rmax[r] = 0.0f;
-        const int64_t row = row_of(i, r);
-#pragma unroll
-        for (int jp = 0; jp < TN / 2; ++jp) {
-          if (FULL || (row < M && cok[jp])) {
-            float g = (float)acc[i][2 * jp][r];
-            g = g * sti[r];
-            g = round_to<OUT>(g * sg[jp]);
-            float u = (float)acc[i][2 * jp + 1][r];
-            u = u * sti[r];
-            u = round_to<OUT>(u * su[jp]);
-            const float e = expf(-g);
-            const float den = 1.0f + e;
-            const float sl = round_to<OUT>(g / den);
-            const float h = round_to<OUT>(sl * u);
-            store_elem<OUT>(p.out, row * p.ldo + hcol[jp], h);
-            rmax[r] = fmaxf(rmax[r], fabsf(h));
-          }
-        }
-      }
-      if (p.row_amax) {
+      for (int jp = 0; jp < TN / 2; ++jp)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float v = rmax[r];
-#pragma unroll
-          for (int o = 1; o < 32; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-          const int64_t row = row_of(i, r);
-          if (lrow == 0 && (FULL || row < M)) atomicMax((unsigned int*)(p.row_amax + row), __float_as_uint(v));
-        }
-      }
-    }
-  } else {
-    float sc[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t col = wcol0 + j * 32 + lrow;
-      sc[j] = (EPI != kEpiRaw && (FULL || col < N)) ? w_scale[col] : 0.0f;
-    }
-    // all token scales / output rows up front when the accumulators leave room, else per block
-    constexpr bool kHoist = TM * TN * 16 > 128;
-    float st_[kHoist ? TM : 1][16];
-    int32_t orow_[kHoist ? TM : 1][16];
-    auto load_rows = [&](int i, float* st, int32_t* orow) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = row_of(i, r);
-        const bool ok = FULL || row < M;
-        if constexpr (MAP) orow[r] = ok ? row_map[row] : -1;
-        else orow[r] = ok ? (int32_t)row : -1;
-        st[r] = (EPI != kEpiRaw && ok) ? a_scale[row] : 0.0f;
-      }
-    };
-    if constexpr (kHoist) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i) load_rows(i, st_[i], orow_[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      if constexpr (!kHoist) load_rows(i, st_[0], orow_[0]);
-      const float* st = st_[kHoist ? i : 0];
-      const int32_t* orow = orow_[kHoist ? i : 0];
-      float res[EPI == kEpiResidual ? 16 : 1][EPI == kEpiResidual ? TN : 1];
-      if constexpr (EPI == kEpiResidual) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            const int64_t col = wcol0 + j * 32 + lrow;
-            res[r][j] = (FULL || (orow[r] >= 0 && col < N)) ? load_elem<OUT>(p.res, (int64_t)orow[r] * p.ldr + col)
-                                                              : 0.0f;
+          const int64_t cg = wcol0 + jp * 64 + (r >> 2) * 8 + lhalf * 4 + (r & 3);  // gate column; up is cg + 32
+          if (rok && cg + 32 < N) {
+            float gv = (float)acc[i][2 * jp][r];
+            gv = gv * st;
+            gv = round_to<OUT>(gv * p.w_scale[cg]);
+            float uv = (float)acc[i][2 * jp + 1][r];
+            uv = uv * st;
+            uv = round_to<OUT>(uv * p.w_scale[cg + 32]);
+            const float e = expf(-gv);
+            const float den = 1.0f + e;
+            const float sl = round_to<OUT>(gv / den);
+            const float h = round_to<OUT>(sl * uv);
+            store_elem<OUT>(p.out, orow * p.ldo + (cg >> 6) * 32 + (cg & 31), h);
+            rmax = fmaxf(rmax, fabsf(h));
           }
+        }
+      if (p.row_amax) {
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+        if (lhalf == 0 && rok) atomicMax((unsigned int*)(p.row_amax + row), __float_as_uint(rmax));
       }
+    } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        if (!FULL && orow[r] < 0) continue;
-        const int64_t obase = (int64_t)orow[r] * p.ldo;
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int64_t col = wcol0 + j * 32 + lrow;
-          if (!FULL && col >= N) continue;
-          if constexpr (EPI == kEpiRaw) {
-            if constexpr (MODE == kInt8) ((int32_t*)p.out)[obase + col] = acc[i][j][r];
-            else ((float*)p.out)[obase + col] = acc[i][j][r];
-          } else {
-            float v = (float)acc[i][j][r];
-            v = v * st[r];
-            v = v * sc[j];
-            if constexpr (EPI == kEpiResidual) {
-              v = round_to<OUT>(v);
-              v = res[r][j] + v;
+        for (int r = 0; r < 16; ++r) {
+          const int64_t col = wcol0 + j * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+          if (rok && col < N) {
+            const int64_t o = orow * p.ldo + col;
+            if constexpr (EPI == kEpiRaw) {
+              if constexpr (MODE == kInt8) ((int32_t*)p.out)[o] = acc[i][j][r];
+              else ((float*)p.out)[o] = acc[i][j][r];
+            } else {
+              float x = (float)acc[i][j][r];
+              x = x * st;
+              x = x * p.w_scale[col];
+              if constexpr (EPI == kEpiResidual) {
+                x = round_to<OUT>(x);
+                x = load_elem<OUT>(p.res, orow * p.ldr + col) + x;
+              }
+              store_elem<OUT>(p.out, o, x);
             }
-            store_elem<OUT>(p.out, obase + col, v);
           }
         }
-      }
     }
   }
 }
 
+// Full-tile epilogue through LDS. For each 32-row block row of the wave tile,
+// every lane writes its runs of 4 finished output values (rounded to OUT) into
+// this wave's LDS region, row-major; the wave then reads the rows back as
+// 16-byte chunks, 16 consecutive lanes per 256-byte row segment, and stores
+// them with 16-byte global stores, so every store instruction writes whole
+// cache lines. The residual (core.py:215: bf16 add of the rounded projection)
+// is applied in the read-back, where its loads are coalesced the same way.
+template <int TN, int EPI, int OUT>
+struct EpiLds {
+  static constexpr int ES = EPI == kEpiRaw ? 4 : (OUT == kF32 ? 4 : 2);  // output element bytes
+  static constexpr int OC = EPI == kEpiSwiGLU ? TN * 16 : TN * 32;        // output columns per wave tile
+  static constexpr int RB = OC * ES;                                      // bytes per output row
+  static constexpr int RS = RB + 16;                                      // padded LDS row stride
+  static constexpr int CPR = RB / 16;                                     // 16-byte chunks per row
+  static constexpr int NRB = 32 * CPR / 64;                               // read-back chunks per lane
+  static constexpr int BYTES = 32 * RS;                                   // LDS bytes per wave
+  static_assert((32 * CPR) % 64 == 0, "read-back split");
+};
+
+template <int OUT, int ES>
+__device__ __forceinline__ void lds_put4(uint8_t* dst, const float* v) {
+  if constexpr (ES == 4) {
+    *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint32_t b[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) b[c] = OUT == kBF16 ? f32_to_bf16_bits(v[c]) : f32_to_f16_bits(v[c]);
+    *(uint2*)dst = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+  }
+}
+
+template <int MODE, int TM, int TN, int EPI, int OUT, bool MAP, typename ACC>
+__device__ __forceinline__ void epilogue_lds(const GemmParams& p, ACC (&acc)[TM][TN], int64_t wrow0, int64_t wcol0,
+                                             int lane, uint8_t* stage) {
+  using E = EpiLds<TN, EPI, OUT>;
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  float st[TM];
+  int64_t orow[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t row = wrow0 + i * 32 + lrow;
+    st[i] = EPI != kEpiRaw ? p.a_scale[row] : 0.0f;
+    if constexpr (MAP) orow[i] = (int64_t)p.row_map[row];
+    else orow[i] = row;
+  }
+  // channel scales: float4 per (block, group); SwiGLU needs the gate and up columns
+  constexpr int NSB = EPI == kEpiRaw ? 1 : TN;
+  float sc[NSB][4][4];
+  if constexpr (EPI != kEpiRaw) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 s4 = *(const float4*)(p.w_scale + wcol0 + j * 32 + g * 8 + lhalf * 4);
+        sc[j][g][0] = s4.x; sc[j][g][1] = s4.y; sc[j][g][2] = s4.z; sc[j][g][3] = s4.w;
+      }
+  }
+  const int64_t ocol0 = EPI == kEpiSwiGLU ? wcol0 / 2 : wcol0;  // first output column of the wave tile
+  uint8_t* my_row = stage + lrow * E::RS;
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    // 1. finish this lane's values of block row i and stage them
+    if constexpr (EPI == kEpiSwiGLU) {
+      float rmax = 0.0f;
+#pragma unroll
+      for (int jp = 0; jp < TN / 2; ++jp)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float h[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            float gv = (float)acc[i][2 * jp][4 * g + c];
+            gv = gv * st[i];
+            gv = round_to<OUT>(gv * sc[2 * jp][g][c]);
+            float uv = (float)acc[i][2 * jp + 1][4 * g + c];
+            uv = uv * st[i];
+            uv = round_to<OUT>(uv * sc[2 * jp + 1][g][c]);
+            const float e = expf(-gv);
+            const float den = 1.0f + e;
+            const float sl = round_to<OUT>(gv / den);
+            h[c] = round_to<OUT>(sl * uv);
+            rmax = fmaxf(rmax, fabsf(h[c]));
+          }
+          lds_put4<OUT, E::ES>(my_row + (jp * 32 + g * 8 + lhalf * 4) * E::ES, h);
+          if (g == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+      if (p.row_amax) {
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));  // lanes l and l + 32 share the row
+        if (lhalf == 0) atomicMax((unsigned int*)(p.row_amax + wrow0 + i * 32 + lrow), __float_as_uint(rmax));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          uint8_t* dst = my_row + (j * 32 + g * 8 + lhalf * 4) * E::ES;
+          if constexpr (EPI == kEpiRaw) {
+            if constexpr (MODE == kInt8)
+              *(int4*)dst = make_int4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+            else
+              *(float4*)dst = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+          } else {
+            float v[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              float x = (float)acc[i][j][4 * g + c];
+              x = x * st[i];
+              v[c] = x * sc[j][g][c];
+            }
+            lds_put4<OUT, E::ES>(dst, v);  // rounds to OUT (the residual adds to the rounded value)
+          }
+          if (g == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // 2. read the staged rows back as 16-byte chunks and store them
+    uint4 chunk[E::NRB];
+    int64_t obase[E::NRB];
+#pragma unroll
+    for (int t = 0; t < E::NRB; ++t) {
+      const int q = t * 64 + lane, r = q / E::CPR, ch = q % E::CPR;
+      chunk[t] = *(const uint4*)(stage + r * E::RS + ch * 16);
+      const int64_t orr = MAP ? __shfl(orow[i], r, 64) : wrow0 + i * 32 + r;
+      obase[t] = orr;
+    }
+    if constexpr (EPI == kEpiResidual) {
+      uint4 rs[E::NRB];
+#pragma unroll
+      for (int t = 0; t < E::NRB; ++t) {
+        const int ch = (t * 64 + lane) % E::CPR;
+        rs[t] = *(const uint4*)((const uint8_t*)p.res + (obase[t] * p.ldr + ocol0) * E::ES + ch * 16);
+      }
+#pragma unroll
+      for (int t = 0; t < E::NRB; ++t) {
+        const uint32_t* a = (const uint32_t*)&chunk[t];
+        const uint32_t* b = (const uint32_t*)&rs[t];
+        uint32_t o[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          if constexpr (E::ES == 4) {
+            o[w] = __float_as_uint(__uint_as_float(b[w]) + __uint_as_float(a[w]));
+          } else {
+            float lo, hi;
+            if constexpr (OUT == kBF16) {
+              lo = bf16_bits_to_f32(b[w] & 0xffffu) + bf16_bits_to_f32(a[w] & 0xffffu);
+              hi = bf16_bits_to_f32(b[w] >> 16) + bf16_bits_to_f32(a[w] >> 16);
+              o[w] = (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+            } else {
+              lo = f16_bits_to_f32(b[w] & 0xffffu) + f16_bits_to_f32(a[w] & 0xffffu);
+              hi = f16_bits_to_f32(b[w] >> 16) + f16_bits_to_f32(a[w] >> 16);
+              o[w] = (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+            }
+          }
+        }
+        chunk[t] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < E::NRB; ++t) {
+      const int ch = (t * 64 + lane) % E::CPR;
+      *(uint4*)((uint8_t*)p.out + (obase[t] * p.ldo + ocol0) * E::ES + ch * 16) = chunk[t];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Full tiles (inside the output, vector-aligned) take the LDS path; edge tiles
+// check and store every element. `stage` is this wave's LDS region
+// (EpiLds::BYTES), free of any in-flight use when the epilogue starts.
 template <int MODE, int TM, int TN, int EPI, int OUT, typename ACC>
 __device__ __forceinline__ void epilogue(const GemmParams& p, ACC (&acc)[TM][TN], int64_t wrow0, int64_t wcol0,
-                                         int lane) {
-  const bool full = wrow0 + TM * 32 <= p.M && wcol0 + TN * 32 <= p.N;
-  if constexpr (EPI == kEpiSwiGLU) {
-    if (full) epilogue_impl<MODE, TM, TN, EPI, OUT, true, false>(p, acc, wrow0, wcol0, lane);
-    else epilogue_impl<MODE, TM, TN, EPI, OUT, false, false>(p, acc, wrow0, wcol0, lane);
-  } else if (p.row_map) {
-    if (full) epilogue_impl<MODE, TM, TN, EPI, OUT, true, true>(p, acc, wrow0, wcol0, lane);
-    else epilogue_impl<MODE, TM, TN, EPI, OUT, false, true>(p, acc, wrow0, wcol0, lane);
+                                         int lane, uint8_t* stage) {
+  const bool full = p.vec && wrow0 + TM * 32 <= p.M && wcol0 + TN * 32 <= p.N;
+  if (full) {
+    if (EPI != kEpiSwiGLU && p.row_map) epilogue_lds<MODE, TM, TN, EPI, OUT, true>(p, acc, wrow0, wcol0, lane, stage);
+    else epilogue_lds<MODE, TM, TN, EPI, OUT, false>(p, acc, wrow0, wcol0, lane, stage);
   } else {
-    if (full) epilogue_impl<MODE, TM, TN, EPI, OUT, true, false>(p, acc, wrow0, wcol0, lane);
-    else epilogue_impl<MODE, TM, TN, EPI, OUT, false, false>(p, acc, wrow0, wcol0, lane);
+    if (EPI != kEpiSwiGLU && p.row_map) epilogue_edge<MODE, TM, TN, EPI, OUT, true>(p, acc, wrow0, wcol0, lane);
+    else epilogue_edge<MODE, TM, TN, EPI, OUT, false>(p, acc, wrow0, wcol0, lane);
   }
 }
 
@@ -347,13 +443,15 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8(GemmParams p) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = MF::run(af[i], bf[j], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = MF::run(bf[j], af[i], acc[i][j]);
     }
     if (kt + 1 < nk) swrite(buf ^ 1);
     __syncthreads();
   }
 
-  epilogue<MODE, TM, TN, EPI, OUT>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane);
+  static_assert(NT / 64 * EpiLds<TN, EPI, OUT>::BYTES <= (int)sizeof(lds), "epilogue staging");
+  epilogue<MODE, TM, TN, EPI, OUT>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
+                                   lds + (tid >> 6) * EpiLds<TN, EPI, OUT>::BYTES);
 }
 
 
@@ -423,6 +521,14 @@ __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F
 // cannot prove disjoint, draining the pipeline); every wait on this DMA is
 // explicit (wait_vmcnt + barrier). M0 holds the LDS address; the s_nop covers
 // the M0-write -> LDS-DMA hazard.
+// A wave-uniform pointer, pinned to SGPRs (the DMA asm takes it as an SGPR pair).
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* q) {
+  const uint64_t v = (uint64_t)(uintptr_t)q;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 template <int OFF>
 __device__ __forceinline__ void dma16(const uint8_t* gbase, uint32_t voff, uint32_t lds_base) {
   asm volatile(
@@ -467,8 +573,8 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
 
   // DMA sources: uniform tile bases + per-lane 32-bit offsets (the host keeps every operand
   // offset below 2^32 for this kernel)
-  const uint8_t* a_base = p.a + m0 * p.lda;
-  const uint8_t* b_base = p.w + n0 * p.ldw;
+  const uint8_t* a_base = uniform_ptr(p.a + m0 * p.lda);
+  const uint8_t* b_base = uniform_ptr(p.w + n0 * p.ldw);
   uint32_t a_off[A_DMA], b_off[B_DMA];
 #pragma unroll
   for (int i = 0; i < A_DMA; ++i) {
@@ -536,7 +642,7 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   auto mfma_q = [&](auto p_c, auto q_c) {
     constexpr int P = decltype(p_c)::value, q = decltype(q_c)::value;
     constexpr int s = q / (TM * TN), i = (q / TN) % TM, j = q % TN;
-    acc[i][j] = MF::run(fa[s][i], fb[P][s][j], acc[i][j]);
+    acc[i][j] = MF::run(fb[P][s][j], fa[s][i], acc[i][j]);
   };
 
   // Step kt with operands in stage U = kt % 4 and B parity P = kt & 1.
@@ -615,7 +721,11 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
     if (kt0 + 3 < nk) step(std::integral_constant<int, 3>{}, Checked{}, kt0 + 3);
   }
 
-  epilogue<MODE, TM, TN, EPI, OUT>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane);
+  // every wave has finished reading the stages before they hold the epilogue's rows
+  wait_lgkm0();
+  lds_barrier();
+  static_assert(NW * EpiLds<TN, EPI, OUT>::BYTES <= (int)sizeof(lds), "epilogue staging");
+  epilogue<MODE, TM, TN, EPI, OUT>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane, lds + wave * EpiLds<TN, EPI, OUT>::BYTES);
 }
 
 // ---------------------------------------------------------------------------

@@ -20,6 +20,7 @@ struct GemmParams {
   int64_t ldr;
   float* row_amax;
   const int32_t* row_map;
+  int vec;  // output, residual and channel scales allow 4-element vector access
   int tiles_m, tiles_n;
 };
 
