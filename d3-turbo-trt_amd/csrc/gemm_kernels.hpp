@@ -762,13 +762,17 @@ static hipError_t launch_dma(GemmParams p, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Tile choice (measured on MI355X): the 4-wave 256x256 DMA tile once there are
+// enough such tiles to cover the chip; 256x128 for mid-size problems; 128x128
+// when even that leaves CUs idle.
 static int choose_tile(int64_t M, int64_t N, int64_t K) {
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
   if (K % kBK2 == 0) {
-    if (t256 >= 256) return kDma256w8;
-    if (t128 >= 192) return kDma128w4;
-    return kTile64x128;
+    if (t256 >= 192) return kDma256w4;
+    if (t256x128 >= 160) return kDma256x128w4;
+    return kDma128w4;
   }
   if (t256 >= 256) return kTile256;
   if (t128 >= 192) return kTile128;
@@ -785,7 +789,7 @@ template <int MODE, int EPI, int OUT>
 hipError_t launch_epi(GemmParams p, int tile, hipStream_t st) {
   if (tile == kTileAuto) {
     tile = choose_tile(p.M, p.N, p.K);
-    if (tile >= kDma256w8 && !dma_offsets_fit(p)) tile = tile == kDma256w8 ? kTile256 : kTile128;
+    if (tile >= kDma256w8 && !dma_offsets_fit(p)) tile = tile == kDma256w4 ? kTile256 : kTile128;
   }
   if (tile >= kDma256w8 && (p.K % kBK2 != 0 || !dma_offsets_fit(p))) return hipErrorInvalidValue;
   switch (tile) {

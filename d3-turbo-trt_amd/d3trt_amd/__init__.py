@@ -3,8 +3,9 @@
 Public API mirrors d3trt/model/quant.py (``MODES``, ``fp8_supported``,
 ``resolve_mode``, ``quantizable``, ``quantize_weight``, ``quantize_rows``,
 ``QuantLinear``, ``make_linear``, ``summarize``) plus the fused MLP block
-(:class:`QuantMLP`). The arithmetic lives in libd3w8a8.so (C ABI:
-include/d3w8a8.h); ``kernels`` holds the thin torch wrappers over it.
+(:class:`QuantMLP`) and the backbone projection stack (:class:`LinearStack`).
+The arithmetic lives in libd3w8a8.so (C ABI: include/d3w8a8.h); ``kernels``
+holds the thin torch wrappers over it.
 """
 
 from .quant import (  # noqa: F401
@@ -19,9 +20,10 @@ from .quant import (  # noqa: F401
     summarize,
 )
 from .mlp import QuantMLP  # noqa: F401
+from .stack import LinearStack  # noqa: F401
 from ._lib import LIB_PATH, LibraryMissing, version  # noqa: F401
 
 __all__ = [
-    "MODES", "QuantLinear", "QuantMLP", "fp8_supported", "make_linear", "quantizable", "quantize_rows",
+    "MODES", "QuantLinear", "QuantMLP", "LinearStack", "fp8_supported", "make_linear", "quantizable", "quantize_rows",
     "quantize_weight", "resolve_mode", "summarize", "LIB_PATH", "LibraryMissing", "version",
 ]

@@ -1,0 +1,129 @@
+"""The W8A8 projection stack of d3's backbone, with the token mixer replaced by identity.
+
+Per layer this is D3Core._layer (d3trt/model/core.py:184-225) with every
+projection quantized (d3trt/model/quant.py) and the attention/GDN mixer left
+out, so that only the linear path runs:
+
+    h   = x + o_proj(mix(qkv_proj(input_norm(x))))       core.py:207-214
+    out = h + down(silu(gate) * up),  gate, up = gate_up(post_norm(h)).chunk(2)
+                                                          core.py:215, trtllm_stack.py:131-134
+
+``mix`` is the identity on the query block: the first ``hidden`` columns of
+the fused [q | k | v] projection are the o_proj input (q_proj's output width
+equals o_proj's input width). The reference runs q/k/v as three projections
+(trtllm_stack.py:79-93); fusing them is a concatenation of weight rows, so
+each output column is the same dot product.
+
+Every layer is eight launches of libd3w8a8 kernels, each one HBM pass:
+norm+quant, QKV GEMM, quant of the q block, o_proj GEMM with the residual
+add, norm+quant, gate_up GEMM with SwiGLU and the row amax, requant, down
+GEMM with the residual add. Question batches (core.py:158-181 runs them
+right-padded) are packed to their valid rows once, run through all layers at
+M = sum(lengths), and scattered back: rows are independent through every
+step, so packing changes no result and computes no padded row.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Sequence
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from . import kernels as K
+from .mlp import QuantMLP
+from .quant import QuantLinear
+
+
+class StackLayer(nn.Module):
+    """One layer's norms and quantized projections."""
+
+    def __init__(self, hidden: int, qkv_out: int, intermediate: int, *, mode: str, dtype: torch.dtype,
+                 device: Any, eps: float = 1e-6):
+        super().__init__()
+        if qkv_out < hidden:
+            raise ValueError("the fused qkv projection must be at least as wide as the hidden size")
+        self.hidden = hidden
+        self.eps = eps
+        self.input_layernorm = nn.Parameter(torch.zeros(hidden, dtype=dtype, device=device), requires_grad=False)
+        self.post_attention_layernorm = nn.Parameter(torch.zeros(hidden, dtype=dtype, device=device),
+                                                     requires_grad=False)
+        self.qkv_proj = QuantLinear(hidden, qkv_out, mode=mode, dtype=dtype, device=device)
+        self.o_proj = QuantLinear(hidden, hidden, mode=mode, dtype=dtype, device=device)
+        self.mlp = QuantMLP(hidden, intermediate, mode=mode, dtype=dtype, device=device)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """[M, hidden] bf16 (rows contiguous) -> [M, hidden]."""
+        mode = self.qkv_proj.mode
+        q1, s1, _ = K.rmsnorm_quantize(x, self.input_layernorm, self.eps, mode)
+        qkv = K.gemm(mode, q1, s1.reshape(-1), self.qkv_proj.weight, self.qkv_proj.weight_scale,
+                     epilogue=_lib.EPI_DEQUANT, out_dtype=x.dtype)
+        q2, s2 = K.quantize_rows(qkv[:, : self.hidden], mode)
+        h = K.gemm(mode, q2, s2.reshape(-1), self.o_proj.weight, self.o_proj.weight_scale,
+                   epilogue=_lib.EPI_RESIDUAL, out_dtype=x.dtype, residual=x)
+        return self.mlp.block(h, self.post_attention_layernorm, self.eps)
+
+
+class LinearStack(nn.Module):
+    """``layers`` x (fused QKV, o_proj, gate_up + SwiGLU, down) with zero-centred RMSNorms."""
+
+    def __init__(self, layers: int, hidden: int, qkv_out: int, intermediate: int, *, mode: str,
+                 dtype: torch.dtype = torch.bfloat16, device: Any = "cuda", eps: float = 1e-6):
+        super().__init__()
+        self.layers = nn.ModuleList(
+            StackLayer(hidden, qkv_out, intermediate, mode=mode, dtype=dtype, device=device, eps=eps)
+            for _ in range(layers)
+        )
+        self.hidden = hidden
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """State pass: [..., hidden] -> [..., hidden] through every layer (M = all rows)."""
+        shape = x.shape
+        h = x.reshape(-1, self.hidden).contiguous()
+        for layer in self.layers:
+            h = layer(h)
+        return h.reshape(shape)
+
+    def forward_ragged(self, x: torch.Tensor, lengths: Sequence[int]) -> torch.Tensor:
+        """Question pass over a right-padded batch [B, W, hidden] with ``lengths[b]`` valid rows.
+
+        The valid rows are packed, run at M = sum(lengths), and scattered back;
+        padded rows of the result are zero (core.py:167-171 zeroes padded
+        inputs; the reference then computes them anyway).
+        """
+        B, W, H = x.shape
+        lengths = [int(n) for n in lengths]
+        if len(lengths) != B or any(n < 0 or n > W for n in lengths):
+            raise ValueError(f"lengths {lengths} do not fit a [{B}, {W}] batch")
+        rows = torch.cat([torch.arange(b * W, b * W + n) for b, n in enumerate(lengths)]) if sum(lengths) else \
+            torch.zeros(0, dtype=torch.long)
+        rows = rows.to(x.device)
+        flat = x.reshape(B * W, H)
+        out = torch.zeros_like(flat)
+        if rows.numel():
+            packed = flat.index_select(0, rows)
+            out.index_copy_(0, rows, self.forward(packed))
+        return out.reshape(B, W, H)
+
+    @torch.no_grad()
+    def init_random(self, generator: torch.Generator, *, weight_std: float = 0.02, norm_std: float = 0.1) -> None:
+        """Random-init every layer: N(0, weight_std) projections (quantized on the GPU), N(0, norm_std)
+        zero-centred norm weights (gain 1 + w)."""
+        for layer in self.layers:
+            dev = layer.qkv_proj.weight.device
+            for lin in (layer.qkv_proj, layer.o_proj):
+                w = torch.randn(lin.out_features, lin.in_features, generator=generator, device=dev,
+                                dtype=torch.float32).mul_(weight_std).to(torch.bfloat16)
+                lin.load_full(w)
+                del w
+            gu, dn = layer.mlp.gate_up_proj, layer.mlp.down_proj
+            w = torch.randn(gu.out_features, gu.in_features, generator=generator, device=dev,
+                            dtype=torch.float32).mul_(weight_std).to(torch.bfloat16)
+            w2 = torch.randn(dn.out_features, dn.in_features, generator=generator, device=dev,
+                             dtype=torch.float32).mul_(weight_std).to(torch.bfloat16)
+            layer.mlp.load_full(w, w2)
+            del w, w2
+            for norm in (layer.input_layernorm, layer.post_attention_layernorm):
+                norm.copy_(torch.randn(norm.shape[0], generator=generator, device=dev,
+                                       dtype=torch.float32).mul_(norm_std))

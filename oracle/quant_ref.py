@@ -241,6 +241,26 @@ def mlp_block(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
                 q2=q2, s2=s2, acc2=acc2, down=down, out=out)
 
 
+def stack_layer(x: torch.Tensor, w_in: torch.Tensor, w_post: torch.Tensor,
+                wqkv_q: torch.Tensor, wqkv_s: torch.Tensor, wo_q: torch.Tensor, wo_s: torch.Tensor,
+                wgu_q: torch.Tensor, wgu_s: torch.Tensor, wd_q: torch.Tensor, wd_s: torch.Tensor,
+                mode: str, eps: float = 1e-6) -> dict:
+    """One backbone layer with the token mixer replaced by identity on the query block.
+
+    D3Core._layer (core.py:205-215): ``h = x + o_proj(mix(qkv_proj(input_layernorm(x))))``,
+    ``out = h + mlp(post_attention_layernorm(h))``, every projection a W8A8 QuantLinear; ``mix``
+    keeps the first ``hidden`` columns of the fused [q | k | v] output. Returns the intermediates.
+    """
+    H = x.shape[1]
+    lin = int8_linear if mode == "int8" else fp8_linear
+    normed = rmsnorm(x, w_in, eps)
+    qkv = lin(normed, wqkv_q, wqkv_s, x.dtype)[0]
+    o = lin(qkv[:, :H], wo_q, wo_s, x.dtype)[0]
+    h = x + o
+    mlp = mlp_block(h, w_post, eps, wgu_q, wgu_s, wd_q, wd_s, mode)
+    return dict(normed=normed, qkv=qkv, o=o, h=h, out=mlp["out"], mlp=mlp)
+
+
 # ---------------------------------------------------------------------------
 # synthetic inputs
 # ---------------------------------------------------------------------------
