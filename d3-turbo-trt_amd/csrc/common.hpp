@@ -63,6 +63,20 @@ __device__ __forceinline__ void store_elem(void* p, int64_t i, float v) {
   else ((float*)p)[i] = v;
 }
 // value as stored in DT and read back (the rounding a torch tensor of that dtype applies)
+// both values as stored in DT and read back; one packed conversion for the pair
+template <int DT>
+__device__ __forceinline__ void round_pair_to(float& a, float& b) {
+  if constexpr (DT == kBF16) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, bf2));  // v_cvt_pk_bf16_f32, RNE
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xffff0000u);
+  } else if constexpr (DT == kF16) {
+    a = f16_bits_to_f32(f32_to_f16_bits(a));
+    b = f16_bits_to_f32(f32_to_f16_bits(b));
+  }
+}
 template <int DT>
 __device__ __forceinline__ float round_to(float v) {
   if constexpr (DT == kBF16) return bf16_round(v);
@@ -71,31 +85,67 @@ __device__ __forceinline__ float round_to(float v) {
 }
 
 // ---- quantization of one value ------------------------------------------------
-// int8: clamp(rint(x / scale), -127, 127)   (quant.py:86, 100)
-__device__ __forceinline__ int quant_i8(float x, float scale) {
-  float q = rintf(x / scale);
-  q = fminf(fmaxf(q, -kInt8Max), kInt8Max);
-  return (int)q;
+// The reference divides every element by its row's fp32 scale (x / scale,
+// quant.py:86, 100). With rd = RN64(1 / scale) formed once per row,
+//   RN32(RN64(x * rd)) == RN32(x / scale)
+// for every finite fp32 x and normal scale: the double product is within
+// 2^-51.9 (relative) of x / scale, while x / scale is either an fp32 value or
+// more than 2^-49 (relative) away from every fp32 rounding midpoint (its
+// distance is a multiple of 2^min(ex, em + es) over a product of at most 49
+// significant bits), and it is never a midpoint itself (x = midpoint * scale
+// would need 25 significant bits in x). Three VALU ops per element replace the
+// ~10 of a correctly rounded fp32 division.
+struct RowScale {
+  float s;
+  double rd;
+};
+__device__ __forceinline__ RowScale make_row_scale(float s) { return RowScale{s, 1.0 / (double)s}; }
+__device__ __forceinline__ float div_row(float x, const RowScale& r) { return (float)((double)x * r.rd); }
+
+// int8: clamp(rint(x / scale), -127, 127) (quant.py:86, 100). Clamping before
+// rounding gives the same integers (127.5 rounds to 128, then clamps to 127;
+// clamped first it stays 127). Adding 1.5 * 2^23 rounds to nearest even and
+// leaves the integer, two's complement, in the low byte of the float's bits.
+__device__ __forceinline__ uint32_t quant_i8_bits(float x, const RowScale& r) {
+  float v = fminf(fmaxf(div_row(x, r), -kInt8Max), kInt8Max);
+  v = v + 12582912.0f;
+  return __float_as_uint(v) & 0xffu;
 }
 // fp8: e4m3fn_rne(clamp(x / scale, -448, 448))   (quant.py:83, 98); the
 // hardware converter rounds to nearest even and is OCP E4M3 on gfx950.
-__device__ __forceinline__ uint32_t quant_f8_pair(float x0, float x1, float scale) {
-  float a = fminf(fmaxf(x0 / scale, -kFp8Max), kFp8Max);
-  float b = fminf(fmaxf(x1 / scale, -kFp8Max), kFp8Max);
+__device__ __forceinline__ uint32_t quant_f8_pair(float x0, float x1, const RowScale& r) {
+  float a = fminf(fmaxf(div_row(x0, r), -kFp8Max), kFp8Max);
+  float b = fminf(fmaxf(div_row(x1, r), -kFp8Max), kFp8Max);
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
 }
 
 // ---- wave reductions (64 lanes) --------------------------------------------------
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+// DPP steps within rows of 16 lanes (row_shr 1, 2, 4, 8), then across rows
+// (row_bcast 15, 31): lane 63 ends up with the reduction of all 64 lanes,
+// which readlane broadcasts through an SGPR. Lanes a step has no source for
+// read 0, so the operation needs op(a, 0) == a: a sum, or a max of values
+// >= 0. Every step is a VALU op; no LDS round trip.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
 }
-__device__ __forceinline__ float wave_sum_tree(float v) {
-  // pairwise tree: lane i adds lane i^o for o = 1, 2, ..., 32 (fixed order)
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) v = v + __shfl_xor(v, o, 64);
-  return v;
+template <typename OP>
+__device__ __forceinline__ float wave_reduce(float v, OP op) {
+  v = op(v, dpp_f32<0x111, 0xf>(v));  // row_shr:1
+  v = op(v, dpp_f32<0x112, 0xf>(v));  // row_shr:2
+  v = op(v, dpp_f32<0x114, 0xf>(v));  // row_shr:4
+  v = op(v, dpp_f32<0x118, 0xf>(v));  // row_shr:8
+  v = op(v, dpp_f32<0x142, 0xa>(v));  // row_bcast:15 into rows 1 and 3
+  v = op(v, dpp_f32<0x143, 0xc>(v));  // row_bcast:31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// max over the wave of values >= 0 (absolute values)
+__device__ __forceinline__ float wave_max(float v) {
+  return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
+}
+// sum over the wave, in the fixed order of the DPP steps above
+__device__ __forceinline__ float wave_sum(float v) {
+  return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 
 }  // namespace d3

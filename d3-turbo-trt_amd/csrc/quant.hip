@@ -16,6 +16,20 @@ namespace d3 {
 
 constexpr int kQuantWaves = 4;  // rows per 256-thread block
 
+// acc + lo^2 + hi^2 of the two 16-bit values packed in w (v_dot2_f32_bf16 / _f16)
+template <int DT>
+__device__ __forceinline__ float dot2_sq(uint32_t w, float acc) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  if constexpr (DT == kBF16) {
+    const bf2 v = __builtin_bit_cast(bf2, w);
+    return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
+  } else {
+    const h2 v = __builtin_bit_cast(h2, w);
+    return __builtin_amdgcn_fdot2(v, v, acc, false);
+  }
+}
+
 // One row of a [*, K] tensor held by one wave: lane l owns the 8-element
 // chunks at columns 512 c + 8 l (c < NCH), kept as raw 16-byte words (32 for
 // fp32) so that a row of 16-bit values costs 4 VGPRs per chunk.
@@ -64,6 +78,42 @@ struct RowChunks {
     }
   }
 
+  // 8 floats -> chunk c in DT (values already representable in DT, as after round_to<DT>)
+  __device__ __forceinline__ void put(int c, const float* v) {
+    if constexpr (DT == kF32) {
+      raw[c][0] = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+      raw[c][1] = make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7]));
+    } else {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = DT == kBF16 ? f32_to_bf16_bits(v[2 * i]) : f32_to_f16_bits(v[2 * i]);
+        const uint32_t hi = DT == kBF16 ? f32_to_bf16_bits(v[2 * i + 1]) : f32_to_f16_bits(v[2 * i + 1]);
+        w[i] = lo | (hi << 16);
+      }
+      raw[c][0] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  // chunk c -> dst (16-byte aligned; 32 bytes for fp32)
+  __device__ __forceinline__ void store_raw(int c, char* dst) const {
+#pragma unroll
+    for (int w = 0; w < kWords; ++w) ((uint4*)dst)[w] = raw[c][w];
+  }
+
+  // Re-materialize the raw words: keeps the compiler from carrying the unpacked floats of the
+  // amax pass into the quantize pass (that would hold 8 VGPRs per chunk instead of 4 and halve
+  // the waves a SIMD can hold).
+  __device__ __forceinline__ void fence() {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int w = 0; w < kWords; ++w) {
+        uint32_t a = raw[c][w].x, b = raw[c][w].y, d = raw[c][w].z, e = raw[c][w].w;
+        asm volatile("" : "+v"(a), "+v"(b), "+v"(d), "+v"(e));
+        raw[c][w] = make_uint4(a, b, d, e);
+      }
+  }
+
   // max |x| over the valid chunks
   __device__ __forceinline__ float amax(int64_t K, int lane) const {
     float m = 0.0f;
@@ -101,25 +151,26 @@ __device__ __forceinline__ void store8(void* p, const float* v) {
 
 // Quantize 8 values with a row scale and store 8 bytes at q.
 template <int MODE>
-__device__ __forceinline__ void quant_store8(void* q, const float* v, float scale) {
+__device__ __forceinline__ void quant_store8(void* q, const float* v, const RowScale& r) {
   uint32_t lo, hi;
   if constexpr (MODE == kInt8) {
     uint32_t b[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) b[i] = (uint32_t)(quant_i8(v[i], scale) & 0xff);
+    for (int i = 0; i < 8; ++i) b[i] = quant_i8_bits(v[i], r);
     lo = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
     hi = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
   } else {
-    lo = quant_f8_pair(v[0], v[1], scale) | (quant_f8_pair(v[2], v[3], scale) << 16);
-    hi = quant_f8_pair(v[4], v[5], scale) | (quant_f8_pair(v[6], v[7], scale) << 16);
+    lo = quant_f8_pair(v[0], v[1], r) | (quant_f8_pair(v[2], v[3], r) << 16);
+    hi = quant_f8_pair(v[4], v[5], r) | (quant_f8_pair(v[6], v[7], r) << 16);
   }
   *(uint2*)q = make_uint2(lo, hi);
 }
 
+// scale = max(amax, 1e-12) / (127 | 448)   (quant.py:95-99: clamp_min, then an fp32 division)
 template <int MODE>
-__device__ __forceinline__ float scale_from_amax(float amax) {
-  amax = fmaxf(amax, kAmaxFloor);  // clamp_min(1e-12)
-  return amax / (MODE == kInt8 ? kInt8Max : kFp8Max);
+__device__ __forceinline__ RowScale scale_from_amax(float amax) {
+  amax = fmaxf(amax, kAmaxFloor);
+  return make_row_scale(amax / (MODE == kInt8 ? kInt8Max : kFp8Max));
 }
 
 // ---------------------------------------------------------------------------
@@ -138,7 +189,8 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ x
   using RC = RowChunks<DT, NCH>;
   RC x_;
   x_.load((const char*)x + row * ldx * RC::kES, K, lane);
-  const float s = scale_from_amax<MODE>(wave_max(x_.amax(K, lane)));
+  const RowScale s = scale_from_amax<MODE>(wave_max(x_.amax(K, lane)));
+  if constexpr (NCH > 12) x_.fence();  // wide rows: keep them packed between the passes (occupancy)
   char* qr = (char*)q + row * ldq;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -148,7 +200,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ x
       quant_store8<MODE>(qr + RC::col(c, lane), v, s);
     }
   }
-  if (lane == 0) scale[row] = s;
+  if (lane == 0) scale[row] = s.s;
 }
 
 // Generic path for any K / alignment: two passes over the row (amax, then quantize).
@@ -163,14 +215,14 @@ __global__ __launch_bounds__(256) void quant_rows_generic(const void* __restrict
   float amax = 0.0f;
   for (int64_t k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(load_elem<DT>(x, base + k)));
   amax = wave_max(amax);
-  const float s = scale_from_amax<MODE>(amax);
+  const RowScale s = scale_from_amax<MODE>(amax);
   uint8_t* qr = (uint8_t*)q + row * ldq;
   for (int64_t k = lane; k < K; k += 64) {
     const float xv = load_elem<DT>(x, base + k);
-    if constexpr (MODE == kInt8) qr[k] = (uint8_t)(quant_i8(xv, s) & 0xff);
+    if constexpr (MODE == kInt8) qr[k] = (uint8_t)quant_i8_bits(xv, s);
     else qr[k] = (uint8_t)(quant_f8_pair(xv, 0.0f, s) & 0xff);
   }
-  if (lane == 0) scale[row] = s;
+  if (lane == 0) scale[row] = s.s;
 }
 
 // ---------------------------------------------------------------------------
@@ -187,7 +239,7 @@ __global__ __launch_bounds__(256) void quant_rows_amax_vec(const void* __restric
   using RC = RowChunks<DT, NCH>;
   RC h_;
   h_.load((const char*)h + row * ldh * RC::kES, K, lane);
-  const float s = scale_from_amax<MODE>(amax_in[row]);
+  const RowScale s = scale_from_amax<MODE>(amax_in[row]);
   char* qr = (char*)q + row * ldq;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -197,20 +249,20 @@ __global__ __launch_bounds__(256) void quant_rows_amax_vec(const void* __restric
       quant_store8<MODE>(qr + RC::col(c, lane), v, s);
     }
   }
-  if (lane == 0) scale[row] = s;
+  if (lane == 0) scale[row] = s.s;
 }
 
 // ---------------------------------------------------------------------------
 // Fused zero-centred RMSNorm + per-token quantization.
 //   y = DT( (x * rstd) * g ),  g = 1 + w (zero_centered) or w,
-//   rstd = 1 / sqrt(sum(x*x) / K + eps)  (correctly rounded), then q(y).
+//   rstd = 1 / sqrt(sum(x*x) / K + eps)  (sqrt and division each correctly rounded), then q(y).
 // Optional: normed output y, and clear_amax[row] = 0 (the SwiGLU amax
 // buffer of the same rows, so the next GEMM can atomically max into it).
 // ---------------------------------------------------------------------------
-template <int MODE, int DT, int DTW, int NCH>
+template <int MODE, int DT, int DTW, int NCH, bool ZC>
 __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
     const void* __restrict__ x, int64_t ldx, const void* __restrict__ w, int64_t M, int64_t K,
-    float eps, int zero_centered, void* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+    float eps, void* __restrict__ q, int64_t ldq, float* __restrict__ scale,
     void* __restrict__ normed, int64_t ldn, float* __restrict__ clear_amax) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
@@ -221,23 +273,31 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
   x_.load((const char*)x + row * ldx * RC::kES, K, lane);
   RW w_;
   w_.load((const char*)w, K, lane);
+  // sum of squares: for 16-bit inputs one v_dot2 per packed pair (the squares of bf16 / fp16 values
+  // are exact in fp32, as torch's x.float().pow(2) is)
   float ss = 0.0f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     if (RC::valid(c, lane, K)) {
-      float v[8];
-      x_.get(c, v);
+      if constexpr (DT == kF32) {
+        float v[8];
+        x_.get(c, v);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float sq = v[i] * v[i];
-        ss = ss + sq;
+        for (int i = 0; i < 8; ++i) {
+          const float sq = v[i] * v[i];
+          ss = ss + sq;
+        }
+      } else {
+        const uint32_t w4[4] = {x_.raw[c][0].x, x_.raw[c][0].y, x_.raw[c][0].z, x_.raw[c][0].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss = dot2_sq<DT>(w4[i], ss);
       }
     }
   }
-  ss = wave_sum_tree(ss);
+  ss = wave_sum(ss);
   const float var = ss / (float)K;
   const float t = var + eps;
-  const float rstd = (float)(1.0 / sqrt((double)t));
+  const float rstd = 1.0f / sqrtf(t);  // torch.rsqrt on the CPU: 1 / sqrt(t), each step correctly rounded
   float y[NCH][8];
   float amax = 0.0f;
 #pragma unroll
@@ -247,15 +307,18 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
       x_.get(c, v);
       w_.get(c, g);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float gain = zero_centered ? (1.0f + g[i]) : g[i];
-        const float nx = v[i] * rstd;
-        y[c][i] = round_to<DT>(nx * gain);
-        amax = fmaxf(amax, fabsf(y[c][i]));
+      for (int i = 0; i < 8; i += 2) {
+        float p0 = v[i] * rstd, p1 = v[i + 1] * rstd;
+        p0 = p0 * (ZC ? 1.0f + g[i] : g[i]);
+        p1 = p1 * (ZC ? 1.0f + g[i + 1] : g[i + 1]);
+        round_pair_to<DT>(p0, p1);
+        y[c][i] = p0;
+        y[c][i + 1] = p1;
+        amax = fmaxf(fmaxf(amax, fabsf(p0)), fabsf(p1));
       }
     }
   }
-  const float s = scale_from_amax<MODE>(wave_max(amax));
+  const RowScale s = scale_from_amax<MODE>(wave_max(amax));
   char* qr = (char*)q + row * ldq;
   char* nr = normed ? (char*)normed + row * ldn * RC::kES : nullptr;
 #pragma unroll
@@ -267,7 +330,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
     }
   }
   if (lane == 0) {
-    scale[row] = s;
+    scale[row] = s.s;
     if (clear_amax) clear_amax[row] = 0.0f;
   }
 }
@@ -308,7 +371,8 @@ __global__ __launch_bounds__(256) void quant_rows_ragged_vec(
   using RC = RowChunks<DT, NCH>;
   RC x_;
   x_.load((const char*)x + prow * ldx * RC::kES, K, lane);
-  const float s = scale_from_amax<MODE>(wave_max(x_.amax(K, lane)));
+  const RowScale s = scale_from_amax<MODE>(wave_max(x_.amax(K, lane)));
+  if constexpr (NCH > 12) x_.fence();  // wide rows: keep them packed between the passes (occupancy)
   char* qr = (char*)q + dst * ldq;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -319,7 +383,7 @@ __global__ __launch_bounds__(256) void quant_rows_ragged_vec(
     }
   }
   if (lane == 0) {
-    scale[dst] = s;
+    scale[dst] = s.s;
     row_map[dst] = (int32_t)prow;
   }
 }
@@ -391,7 +455,9 @@ hipError_t launch_rmsnorm_quant_t(const void* x, int64_t ldx, const void* w, int
                                   int zc, void* q, int64_t ldq, float* scale, void* normed, int64_t ldn,
                                   float* clear_amax, hipStream_t st) {
   if (M == 0) return hipSuccess;
-#define L(N) hipLaunchKernelGGL((rmsnorm_quant_vec<MODE, DT, DTW, N>), quant_grid(M), dim3(256), 0, st, x, ldx, w, M, K, eps, zc, q, ldq, scale, normed, ldn, clear_amax)
+#define L(N)                                                                                                        \
+  if (zc) hipLaunchKernelGGL((rmsnorm_quant_vec<MODE, DT, DTW, N, true>), quant_grid(M), dim3(256), 0, st, x, ldx, w, M, K, eps, q, ldq, scale, normed, ldn, clear_amax); \
+  else hipLaunchKernelGGL((rmsnorm_quant_vec<MODE, DT, DTW, N, false>), quant_grid(M), dim3(256), 0, st, x, ldx, w, M, K, eps, q, ldq, scale, normed, ldn, clear_amax)
   D3_NCH_DISPATCH(K, L);
 #undef L
   return hipGetLastError();
