@@ -10,6 +10,8 @@
 #include "kernels.hpp"
 #include "../../include/d3w8a8.h"
 
+static_assert(d3::kMaxSegments == D3W8A8_MAX_SEGMENTS, "segment limit of the C ABI and the kernels");
+
 namespace {
 
 thread_local char g_err[512] = "";
@@ -97,12 +99,21 @@ int d3w8a8_quantize_rows_ragged(int mode, int in_dtype, const void* x, int64_t l
   if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "quantize_rows_ragged: unknown mode %d", mode);
   if (!dtype_ok(in_dtype) || (out && !dtype_ok(out_dtype)))
     return fail(D3W8A8_EINVAL, "quantize_rows_ragged: unknown dtype");
-  if (nseg < 0 || width < 0 || K < 8 || K % 8 != 0 || K > d3::kMaxVecK || ldx < K || ldq < K)
-    return fail(D3W8A8_EINVAL, "quantize_rows_ragged: bad shape nseg=%lld width=%lld K=%lld", (long long)nseg,
-                (long long)width, (long long)K);
+  if (nseg < 0 || nseg > D3W8A8_MAX_SEGMENTS || width < 0 || K < 8 || K % 8 != 0 || K > d3::kMaxVecK || ldx < K ||
+      ldq < K)
+    return fail(D3W8A8_EINVAL, "quantize_rows_ragged: bad shape nseg=%lld (at most %d) width=%lld K=%lld",
+                (long long)nseg, D3W8A8_MAX_SEGMENTS, (long long)width, (long long)K);
   if (nseg * width > INT32_MAX) return fail(D3W8A8_EINVAL, "quantize_rows_ragged: too many rows");
   if (nseg == 0 || width == 0) return D3W8A8_OK;
   if (!x || !lengths || !q || !scale || !row_map) return fail(D3W8A8_EINVAL, "quantize_rows_ragged: null pointer");
+  d3::SegOffsets segs;
+  segs.off[0] = 0;
+  for (int64_t b = 0; b < nseg; ++b) {
+    if (lengths[b] < 0 || lengths[b] > width)
+      return fail(D3W8A8_EINVAL, "quantize_rows_ragged: length %d of segment %lld outside [0, %lld]", lengths[b],
+                  (long long)b, (long long)width);
+    segs.off[b + 1] = segs.off[b] + lengths[b];
+  }
   const int es = esize(in_dtype), va = es == 4 ? 32 : 16;
   if ((ldx * es) % va || !aligned(x, va) || ldq % 8 || !aligned(q, 8))
     return fail(D3W8A8_EINVAL, "quantize_rows_ragged: rows must be 16-byte aligned");
@@ -112,7 +123,7 @@ int d3w8a8_quantize_rows_ragged(int mode, int in_dtype, const void* x, int64_t l
     if (N < 1 || ldo < N || (N * oes) % 16 || (ldo * oes) % 16 || !aligned(out, 16))
       return fail(D3W8A8_EINVAL, "quantize_rows_ragged: output rows must be 16-byte multiples and aligned");
   }
-  return hip_status(d3::launch_quant_ragged(mode, in_dtype, oes, x, ldx, lengths, nseg, width, K, q, ldq, scale,
+  return hip_status(d3::launch_quant_ragged(mode, in_dtype, oes, x, ldx, segs, nseg, width, K, q, ldq, scale,
                                             row_map, out, ldo, N, (hipStream_t)stream),
                     "quantize_rows_ragged");
 }

@@ -31,7 +31,14 @@ hipError_t launch_quant_rows_amax(int mode, int dt, const void* h, int64_t ldh, 
 hipError_t launch_rmsnorm_quant(int mode, int dt, int dtw, const void* x, int64_t ldx, const void* w, int64_t M,
                                 int64_t K, float eps, int zc, void* q, int64_t ldq, float* scale, void* normed,
                                 int64_t ldn, float* clear_amax, hipStream_t st);
-hipError_t launch_quant_ragged(int mode, int dt, int out_es, const void* x, int64_t ldx, const int32_t* lengths,
+// Packed-row offsets of a ragged batch, passed by value in the kernel arguments:
+// segment b owns packed rows [off[b], off[b + 1]).
+constexpr int kMaxSegments = 256;
+struct SegOffsets {
+  int32_t off[kMaxSegments + 1];
+};
+
+hipError_t launch_quant_ragged(int mode, int dt, int out_es, const void* x, int64_t ldx, const SegOffsets& segs,
                                int64_t nseg, int64_t width, int64_t K, void* q, int64_t ldq, float* scale,
                                int32_t* row_map, void* out, int64_t ldo, int64_t N, hipStream_t st);
 hipError_t launch_gemm(int mode, GemmParams p, int epi, int out_dt, int tile, hipStream_t st);

@@ -337,27 +337,24 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
 
 // ---------------------------------------------------------------------------
 // Ragged gather: x is the right-padded [nseg, width, K] question batch;
-// segment b holds lengths[b] valid rows. Valid row (b, t) is quantized into
-// packed row off(b) + t, off(b) = lengths[0] + ... + lengths[b-1], and
-// row_map[packed] = b * width + t. Padded rows (t >= lengths[b]) instead get
-// their output row zeroed (out [nseg*width, N] of out_dtype, ld ldo), so the
-// GEMM, which only visits packed rows, leaves a fully defined output.
+// segment b holds off[b+1] - off[b] valid rows. Valid row (b, t) is quantized
+// into packed row off[b] + t and row_map[packed] = b * width + t. Padded rows
+// (t >= length) instead get their output row zeroed (out [nseg*width, N] of
+// out_dtype, ld ldo), so the GEMM, which only visits packed rows, leaves a
+// fully defined output. The offsets travel by value in the kernel arguments:
+// no host-to-device copy precedes the launch, and a captured graph keeps them.
 // ---------------------------------------------------------------------------
 template <int MODE, int DT, int NCH, int OUTES>
 __global__ __launch_bounds__(256) void quant_rows_ragged_vec(
-    const void* __restrict__ x, int64_t ldx, const int32_t* __restrict__ lengths, int64_t nseg,
+    const void* __restrict__ x, int64_t ldx, const SegOffsets segs, int64_t nseg,
     int64_t width, int64_t K, void* __restrict__ q, int64_t ldq, float* __restrict__ scale,
     int32_t* __restrict__ row_map, void* __restrict__ out, int64_t ldo, int64_t N) {
   const int lane = threadIdx.x & 63;
   const int64_t prow = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
   if (prow >= nseg * width) return;
   const int64_t b = prow / width, t = prow - b * width;
-  // offset of segment b: wave-parallel sum of lengths[0..b)
-  int64_t part = 0;
-  for (int64_t i = lane; i < b; i += 64) part += lengths[i];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
-  const int64_t len = lengths[b];
+  const int64_t part = segs.off[b];
+  const int64_t len = segs.off[b + 1] - part;
   if (t >= len) {
     if (out) {
       // the host guarantees 16-byte aligned output rows and N * OUTES % 16 == 0
@@ -475,22 +472,22 @@ hipError_t launch_rmsnorm_quant(int mode, int dt, int dtw, const void* x, int64_
 }
 
 template <int MODE, int DT, int OUTES>
-hipError_t launch_quant_ragged_t(const void* x, int64_t ldx, const int32_t* lengths, int64_t nseg, int64_t width,
+hipError_t launch_quant_ragged_t(const void* x, int64_t ldx, const SegOffsets& segs, int64_t nseg, int64_t width,
                                  int64_t K, void* q, int64_t ldq, float* scale, int32_t* row_map, void* out,
                                  int64_t ldo, int64_t N, hipStream_t st) {
   const int64_t rows = nseg * width;
   if (rows == 0) return hipSuccess;
-#define L(NC) hipLaunchKernelGGL((quant_rows_ragged_vec<MODE, DT, NC, OUTES>), quant_grid(rows), dim3(256), 0, st, x, ldx, lengths, nseg, width, K, q, ldq, scale, row_map, out, ldo, N)
+#define L(NC) hipLaunchKernelGGL((quant_rows_ragged_vec<MODE, DT, NC, OUTES>), quant_grid(rows), dim3(256), 0, st, x, ldx, segs, nseg, width, K, q, ldq, scale, row_map, out, ldo, N)
   D3_NCH_DISPATCH(K, L);
 #undef L
   return hipGetLastError();
 }
 
-hipError_t launch_quant_ragged(int mode, int dt, int out_es, const void* x, int64_t ldx, const int32_t* lengths,
+hipError_t launch_quant_ragged(int mode, int dt, int out_es, const void* x, int64_t ldx, const SegOffsets& segs,
                                int64_t nseg, int64_t width, int64_t K, void* q, int64_t ldq, float* scale,
                                int32_t* row_map, void* out, int64_t ldo, int64_t N, hipStream_t st) {
   if (K > kMaxVecK) return hipErrorInvalidValue;
-#define C(MO, D, E) if (mode == MO && dt == D && out_es == E) return launch_quant_ragged_t<MO, D, E>(x, ldx, lengths, nseg, width, K, q, ldq, scale, row_map, out, ldo, N, st)
+#define C(MO, D, E) if (mode == MO && dt == D && out_es == E) return launch_quant_ragged_t<MO, D, E>(x, ldx, segs, nseg, width, K, q, ldq, scale, row_map, out, ldo, N, st)
   C(kInt8, kBF16, 2); C(kInt8, kBF16, 4); C(kInt8, kF16, 2); C(kInt8, kF16, 4); C(kInt8, kF32, 2); C(kInt8, kF32, 4);
   C(kFp8, kBF16, 2); C(kFp8, kBF16, 4); C(kFp8, kF16, 2); C(kFp8, kF16, 4); C(kFp8, kF32, 2); C(kFp8, kF32, 4);
 #undef C

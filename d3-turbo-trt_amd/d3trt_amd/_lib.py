@@ -19,6 +19,7 @@ INT8, FP8 = 0, 1
 BF16, F16, F32 = 0, 1, 2
 EPI_DEQUANT, EPI_RAW, EPI_SWIGLU, EPI_RESIDUAL = 0, 1, 2, 3
 TILE_AUTO, TILE_256, TILE_128, TILE_64x128 = -1, 0, 1, 2
+MAX_SEGMENTS = 256  # D3W8A8_MAX_SEGMENTS: blocks of one ragged batch
 TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4 = 3, 4, 5, 6
 TILES = (TILE_256, TILE_128, TILE_64x128, TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4)
 DMA_TILES = (TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4)

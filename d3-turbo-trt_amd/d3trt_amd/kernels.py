@@ -6,6 +6,7 @@ stream. There is no CPU implementation behind any of them.
 
 from __future__ import annotations
 
+import ctypes
 from typing import Optional, Sequence
 
 import torch
@@ -114,10 +115,12 @@ def quantize_rows_amax(h: torch.Tensor, amax: torch.Tensor, mode: str):
 
 def quantize_rows_ragged(x: torch.Tensor, lengths: Sequence[int], mode: str, *,
                          out: Optional[torch.Tensor] = None):
-    """Right-padded [B, W, K] -> packed (q [T, K], scale [T, 1], row_map [T] int32).
+    """Right-padded [B, W, K] -> packed (q [T, K], scale [T, 1], row_map [T] int32), T = sum(lengths).
 
-    T = sum(lengths). When ``out`` ([B*W, N] view of the final output) is given,
-    its padded rows are zeroed.
+    The lengths stay on the host: the library folds them into packed-row
+    offsets passed to the kernel by value (no host-to-device copy, so the call
+    can be captured in a graph). When ``out`` ([B*W, N] view of the final
+    output) is given, its padded rows are zeroed.
     """
     _gpu(x, "x")
     if x.dim() != 3:
@@ -126,11 +129,13 @@ def quantize_rows_ragged(x: torch.Tensor, lengths: Sequence[int], mode: str, *,
     lengths = [int(n) for n in lengths]
     if len(lengths) != B or any(n < 0 or n > W for n in lengths):
         raise ValueError(f"lengths {lengths} do not fit a [{B}, {W}] batch")
+    if B > _lib.MAX_SEGMENTS:
+        raise ValueError(f"at most {_lib.MAX_SEGMENTS} blocks per ragged batch, got {B}")
     x2 = x.reshape(B * W, K)
     x2 = _rows(x2, "x")
     T = sum(lengths)
     dev = x.device
-    lens = torch.tensor(lengths, dtype=torch.int32).to(dev, non_blocking=False)
+    host_lengths = (ctypes.c_int32 * max(B, 1))(*lengths)
     # at least one row so the pointers are valid when every block is empty (the kernel
     # still runs to zero the padded output rows)
     q = torch.empty(max(T, 1), K, dtype=qdtype(mode), device=dev)
@@ -139,12 +144,12 @@ def quantize_rows_ragged(x: torch.Tensor, lengths: Sequence[int], mode: str, *,
     N = out.shape[1] if out is not None else 0
     lib = _lib.load()
     rc = lib.d3w8a8_quantize_rows_ragged(
-        mode_code(mode), dtype_code(x2.dtype), x2.data_ptr(), x2.stride(0), lens.data_ptr(), B, W, K,
-        q.data_ptr(), K, s.data_ptr(), row_map.data_ptr(), _ptr(out),
+        mode_code(mode), dtype_code(x2.dtype), x2.data_ptr(), x2.stride(0), ctypes.addressof(host_lengths), B, W,
+        K, q.data_ptr(), K, s.data_ptr(), row_map.data_ptr(), _ptr(out),
         dtype_code(out.dtype) if out is not None else 0, out.stride(0) if out is not None else 0, N,
         _stream(x2))
     _lib.check(rc, "quantize_rows_ragged")
-    return q[:T], s[:T], row_map[:T], lens
+    return q[:T], s[:T], row_map[:T]
 
 
 def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.Tensor,

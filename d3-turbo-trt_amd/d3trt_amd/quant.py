@@ -168,7 +168,7 @@ class QuantLinear(nn.Module):
         B, W, _ = x.shape
         out = torch.empty(B, W, self.out_features, dtype=self.dtype, device=x.device)
         out2 = out.view(B * W, self.out_features)
-        q, s, row_map, _lens = K.quantize_rows_ragged(x, lengths, self.mode, out=out2)
+        q, s, row_map = K.quantize_rows_ragged(x, lengths, self.mode, out=out2)
         if q.shape[0]:
             K.gemm(self.mode, q, s.reshape(-1), self.weight, self.weight_scale, epilogue=_lib.EPI_DEQUANT,
                    out_dtype=self.dtype, out=out2, row_map=row_map)

@@ -85,26 +85,43 @@ class LinearStack(nn.Module):
             h = layer(h)
         return h.reshape(shape)
 
-    def forward_ragged(self, x: torch.Tensor, lengths: Sequence[int]) -> torch.Tensor:
+    def forward_ragged(self, x: torch.Tensor, lengths: Sequence[int], *, graph: bool = False) -> torch.Tensor:
         """Question pass over a right-padded batch [B, W, hidden] with ``lengths[b]`` valid rows.
 
         The valid rows are packed, run at M = sum(lengths), and scattered back;
         padded rows of the result are zero (core.py:167-171 zeroes padded
-        inputs; the reference then computes them anyway).
+        inputs; the reference then computes them anyway). With ``graph=True``
+        the packed pass replays a HIP graph captured once per row count
+        (:class:`GraphedStack`), so the ~8 launches per layer cost one launch.
         """
         B, W, H = x.shape
         lengths = [int(n) for n in lengths]
         if len(lengths) != B or any(n < 0 or n > W for n in lengths):
             raise ValueError(f"lengths {lengths} do not fit a [{B}, {W}] batch")
-        rows = torch.cat([torch.arange(b * W, b * W + n) for b, n in enumerate(lengths)]) if sum(lengths) else \
-            torch.zeros(0, dtype=torch.long)
-        rows = rows.to(x.device)
+        rows = self._packed_rows(tuple(lengths), W, x.device)
         flat = x.reshape(B * W, H)
         out = torch.zeros_like(flat)
         if rows.numel():
             packed = flat.index_select(0, rows)
-            out.index_copy_(0, rows, self.forward(packed))
+            res = self.graphed(rows.numel())(packed) if graph else self.forward(packed)
+            out.index_copy_(0, rows, res)
         return out.reshape(B, W, H)
+
+    def _packed_rows(self, lengths: tuple, width: int, device) -> torch.Tensor:
+        """Device indices of the valid rows of a [B, width] batch (cached per shape)."""
+        cache = self.__dict__.setdefault("_rows_cache", {})
+        key = (lengths, width, str(device))
+        if key not in cache:
+            idx = [b * width + t for b, n in enumerate(lengths) for t in range(n)]
+            cache[key] = torch.tensor(idx, dtype=torch.long).to(device)
+        return cache[key]
+
+    def graphed(self, rows: int) -> "GraphedStack":
+        """The HIP-graph replay of :meth:`forward` for ``rows`` packed rows (captured on first use)."""
+        graphs = self.__dict__.setdefault("_graphs", {})
+        if rows not in graphs:
+            graphs[rows] = GraphedStack(self, rows)
+        return graphs[rows]
 
     @torch.no_grad()
     def init_random(self, generator: torch.Generator, *, weight_std: float = 0.02, norm_std: float = 0.1) -> None:
@@ -127,3 +144,33 @@ class LinearStack(nn.Module):
             for norm in (layer.input_layernorm, layer.post_attention_layernorm):
                 norm.copy_(torch.randn(norm.shape[0], generator=generator, device=dev,
                                        dtype=torch.float32).mul_(norm_std))
+
+
+class GraphedStack:
+    """:meth:`LinearStack.forward` on a fixed number of rows, captured as one HIP graph.
+
+    A question batch runs every layer at a small M (e.g. 8 blocks x 16 tokens),
+    where each of the ~8 launches per layer is cheaper on the GPU than on the
+    host. The capture records the same kernels the eager pass launches (no
+    memset or host copy happens inside it); a call copies the input into the
+    static buffer, replays, and returns the static output, which the next call
+    overwrites.
+    """
+
+    def __init__(self, stack: LinearStack, rows: int):
+        dev = next(stack.buffers()).device
+        self.static_in = torch.zeros(rows, stack.hidden, dtype=torch.bfloat16, device=dev)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(2):  # warm the allocator outside the capture
+                stack.forward(self.static_in)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.static_out = stack.forward(self.static_in)
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        self.static_in.copy_(x)
+        self.graph.replay()
+        return self.static_out

@@ -88,9 +88,12 @@ int d3w8a8_quantize_rows_amax(int mode, int in_dtype, const void* h, int64_t ldh
 /* Ragged gather-quantize for a right-padded question batch x [nseg, width, K]
  * (backends/trtllm.py:149-179 builds such batches; core.py:158-181 runs them):
  * valid row (b, t < lengths[b]) is quantized into packed row off(b) + t with
- * row_map[off(b) + t] = b * width + t; padded rows of `out` (optional,
- * [nseg * width, N] of out_dtype, ld ldo) are zeroed. lengths is a device
- * int32 array of nseg entries. */
+ * row_map[off(b) + t] = b * width + t, off(b) = lengths[0] + ... + lengths[b-1];
+ * padded rows of `out` (optional, [nseg * width, N] of out_dtype, ld ldo) are
+ * zeroed. `lengths` is a HOST array of nseg <= D3W8A8_MAX_SEGMENTS entries,
+ * read during the call and passed to the kernel by value: no host-to-device
+ * copy precedes the launch. */
+#define D3W8A8_MAX_SEGMENTS 256
 int d3w8a8_quantize_rows_ragged(int mode, int in_dtype, const void* x, int64_t ldx, const int32_t* lengths,
                                 int64_t nseg, int64_t width, int64_t K, void* q, int64_t ldq, float* scale,
                                 int32_t* row_map, void* out, int out_dtype, int64_t ldo, int64_t N,

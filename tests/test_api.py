@@ -117,3 +117,19 @@ def test_gate_up_interleave_roundtrip():
     assert torch.equal(K.deinterleave_gate_up(il), w)
     with pytest.raises(ValueError):
         K.interleave_gate_up(torch.zeros(96, 2))
+
+
+def test_ragged_lengths_are_checked_on_the_host():
+    """Segment lengths travel by value; bad ones are refused before any launch."""
+    import ctypes
+    lib = _lib.load()
+    dummy = 256  # never dereferenced: every call below fails in the host-side checks
+    bad_len = (ctypes.c_int32 * 2)(3, 9)   # 9 > width 8
+    assert lib.d3w8a8_quantize_rows_ragged(0, 0, dummy, 64, ctypes.addressof(bad_len), 2, 8, 64, dummy, 64, dummy,
+                                           dummy, None, 0, 0, 0, None) == _lib.EINVAL
+    assert b"length 9" in lib.d3w8a8_last_error()
+    many = (ctypes.c_int32 * 300)(*([1] * 300))
+    assert lib.d3w8a8_quantize_rows_ragged(0, 0, dummy, 64, ctypes.addressof(many), 300, 8, 64, dummy, 64, dummy,
+                                           dummy, None, 0, 0, 0, None) == _lib.EINVAL
+    header = open(os.path.join(ROOT, "include", "d3w8a8.h")).read()
+    assert re.search(r"#define D3W8A8_MAX_SEGMENTS (\d+)", header).group(1) == str(_lib.MAX_SEGMENTS)

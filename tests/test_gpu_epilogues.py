@@ -127,7 +127,7 @@ def test_ragged_equals_separate_blocks(dev, mode):
         assert torch.equal(out[b, :n], sep)
         assert torch.all(out[b, n:] == 0)
     if mode == "int8":
-        q, s, row_map, _ = K.quantize_rows_ragged(xd, lengths, mode)
+        q, s, row_map = K.quantize_rows_ragged(xd, lengths, mode)
         raw = K.gemm(mode, q, None, lin.weight, None, epilogue=_lib.EPI_RAW).cpu()
         start = 0
         for b, n in enumerate(lengths):

@@ -87,3 +87,34 @@ def test_stack_two_layers_fp8_against_oracle(dev):
         ref = R.stack_layer(ref, mode="fp8", **_oracle_weights(layer, "fp8"))["out"]
     assert rel_err(out - x, ref - x) < 3e-2
     assert float((bf16_ulp_diff(out, ref) <= 2).float().mean()) > 0.9
+
+
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
+def test_graph_replays_match_eager(dev, mode):
+    """Each replay of the captured stack equals the eager pass on the same input, with eager work and
+    synchronizations between the replays."""
+    st = _stack(dev, 2, mode, 4)
+    g = gen(10)
+    xs = [R.outlier_activations(g, 48, H).to(dev) for _ in range(3)]
+    graphed = st.graphed(48)
+    for x in xs:
+        eager = st(x).clone()
+        st(xs[0])  # unrelated eager work between replays
+        torch.cuda.synchronize()
+        out = graphed(x).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
+def test_graphed_ragged_pass_equals_eager(dev):
+    st = _stack(dev, 2, "int8", 5)
+    g = gen(11)
+    lengths = [16, 3, 16, 0, 9]
+    x = torch.zeros(len(lengths), 16, H, dtype=torch.bfloat16)
+    for b, n in enumerate(lengths):
+        if n:
+            x[b, :n] = R.outlier_activations(g, n, H)
+    xd = x.to(dev)
+    eager = st.forward_ragged(xd, lengths).clone()
+    for _ in range(3):
+        assert torch.equal(st.forward_ragged(xd, lengths, graph=True), eager)
