@@ -128,20 +128,18 @@ int d3w8a8_quantize_rows_ragged(int mode, int in_dtype, const void* x, int64_t l
                     "quantize_rows_ragged");
 }
 
-int d3w8a8_gemm(int mode, const void* a, int64_t lda, const float* a_scale, const void* w, int64_t ldw,
-                const float* w_scale, int64_t M, int64_t N, int64_t K, int epilogue, int out_dtype, void* out,
-                int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
-                void* stream) {
+static int gemm_impl(int mode, const void* a, int64_t lda, const float* a_scale, const void* w, int64_t ldw,
+                     const float* w_scale, int64_t M, int64_t N, int64_t K, int epilogue, int out_dtype, void* out,
+                     int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
+                     int ksplit, void* workspace, int64_t workspace_bytes, void* stream) {
   if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "gemm: unknown mode %d", mode);
   if (epilogue < D3W8A8_EPI_DEQUANT || epilogue > D3W8A8_EPI_RESIDUAL)
     return fail(D3W8A8_EINVAL, "gemm: unknown epilogue %d", epilogue);
   if (epilogue != D3W8A8_EPI_RAW && !dtype_ok(out_dtype)) return fail(D3W8A8_EINVAL, "gemm: unknown out dtype");
   if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_256x128_W4) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
-  if (tile >= D3W8A8_TILE_DMA_256_W8 && K % 64 != 0)
-    return fail(D3W8A8_EINVAL, "gemm: the pipelined tiles need K %% 64 == 0");
-  if (tile >= D3W8A8_TILE_DMA_256_W8 && ((M > 0 && (M - 1) * lda + K >= ((int64_t)1 << 32)) ||
-                                         (N > 0 && (N - 1) * ldw + K >= ((int64_t)1 << 32))))
-    return fail(D3W8A8_EINVAL, "gemm: the pipelined tiles address each operand with 32-bit offsets");
+  if (ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) return fail(D3W8A8_EINVAL, "gemm: bad ksplit %d", ksplit);
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && (!workspace || !aligned(workspace, 256))))
+    return fail(D3W8A8_EINVAL, "gemm: the workspace must be 256-byte aligned device memory");
   if (M < 0 || N < 0 || K < 0 || K % 16 != 0)
     return fail(D3W8A8_EINVAL, "gemm: bad shape M=%lld N=%lld K=%lld (K must be a multiple of 16)", (long long)M,
                 (long long)N, (long long)K);
@@ -149,6 +147,8 @@ int d3w8a8_gemm(int mode, const void* a, int64_t lda, const float* a_scale, cons
   const int64_t ncols = epilogue == D3W8A8_EPI_SWIGLU ? N / 2 : N;
   if (lda < K || ldw < K || lda % 16 || ldw % 16 || ldo < ncols)
     return fail(D3W8A8_EINVAL, "gemm: leading dimensions must cover the rows and be multiples of 16");
+  const d3::GemmPlan plan = d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, workspace_bytes);
+  if (plan.error) return fail(D3W8A8_EINVAL, "gemm: %s", plan.error);
   if (M == 0 || N == 0) return D3W8A8_OK;
   if (!a || !w || !out || (epilogue != D3W8A8_EPI_RAW && (!a_scale || !w_scale)))
     return fail(D3W8A8_EINVAL, "gemm: null pointer");
@@ -164,11 +164,43 @@ int d3w8a8_gemm(int mode, const void* a, int64_t lda, const float* a_scale, cons
   p.M = M; p.N = N; p.K = K;
   p.out = out; p.ldo = ldo; p.res = res; p.ldr = ldr;
   p.row_amax = row_amax; p.row_map = row_map;
+  p.partial = (uint32_t*)workspace;
   const int oes = epilogue == D3W8A8_EPI_RAW ? 4 : esize(out_dtype);
   // full tiles store 16-byte row chunks: rows of out (and res) must be 16-byte aligned
   p.vec = (ldo * oes) % 16 == 0 && aligned(out, 16) && (epilogue == D3W8A8_EPI_RAW || aligned(w_scale, 16)) &&
           (epilogue != D3W8A8_EPI_RESIDUAL || ((ldr * oes) % 16 == 0 && aligned(res, 16)));
-  return hip_status(d3::launch_gemm(mode, p, epilogue, out_dtype, tile, (hipStream_t)stream), "gemm");
+  return hip_status(d3::launch_gemm(mode, p, epilogue, out_dtype, plan, (hipStream_t)stream), "gemm");
+}
+
+int d3w8a8_gemm(int mode, const void* a, int64_t lda, const float* a_scale, const void* w, int64_t ldw,
+                const float* w_scale, int64_t M, int64_t N, int64_t K, int epilogue, int out_dtype, void* out,
+                int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
+                void* stream) {
+  return gemm_impl(mode, a, lda, a_scale, w, ldw, w_scale, M, N, K, epilogue, out_dtype, out, ldo, res, ldr,
+                   row_amax, row_map, tile, 1, nullptr, 0, stream);
+}
+
+int d3w8a8_gemm_ws(int mode, const void* a, int64_t lda, const float* a_scale, const void* w, int64_t ldw,
+                   const float* w_scale, int64_t M, int64_t N, int64_t K, int epilogue, int out_dtype, void* out,
+                   int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
+                   int ksplit, void* workspace, int64_t workspace_bytes, void* stream) {
+  return gemm_impl(mode, a, lda, a_scale, w, ldw, w_scale, M, N, K, epilogue, out_dtype, out, ldo, res, ldr,
+                   row_amax, row_map, tile, ksplit, workspace, workspace_bytes, stream);
+}
+
+int64_t d3w8a8_gemm_workspace(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
+                              int64_t max_bytes) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 16 || lda < K || ldw < K || M > INT32_MAX / 2 || N > INT32_MAX / 2 ||
+      tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_256x128_W4 || ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) {
+    fail(D3W8A8_EINVAL, "gemm_workspace: bad arguments");
+    return -1;
+  }
+  const d3::GemmPlan plan = d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, max_bytes < 0 ? 0 : max_bytes);
+  if (plan.error) {
+    fail(D3W8A8_EINVAL, "gemm_workspace: %s", plan.error);
+    return -1;
+  }
+  return plan.ws_bytes;
 }
 
 }  // extern "C"

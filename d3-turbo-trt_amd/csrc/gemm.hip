@@ -4,6 +4,8 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
+
 namespace d3 {
 
 template <int MODE, int EPI, int OUT>
@@ -44,9 +46,105 @@ static hipError_t launch_mode(GemmParams p, int epi, int out_dt, int tile, hipSt
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemm(int mode, GemmParams p, int epi, int out_dt, int tile, hipStream_t st) {
+namespace {
+
+struct TileShape {
+  int bm, bn;
+  bool dma;
+  int per_cu;  // workgroups one CU holds at once (LDS: 4 stages of (bm + bn) x 64 bytes)
+};
+
+TileShape shape_of(int tile) {
+  switch (tile) {
+    case kTile256: return {256, 256, false, 1};
+    case kTile128: return {128, 128, false, 1};
+    case kTile64x128: return {64, 128, false, 1};
+    case kDma256w8: return {256, 256, true, 1};
+    case kDma256w4: return {256, 256, true, 1};
+    case kDma128w4: return {128, 128, true, 2};
+    case kDma256x128w4: return {256, 128, true, 1};
+  }
+  return {0, 0, false, 0};
+}
+
+constexpr int kCUs = 256;          // MI355X compute units
+constexpr int kMinSplitSteps = 4;  // K steps (64 bytes each) per split at least
+
+// The DMA kernels address operands as a tile base plus a 32-bit per-lane offset.
+bool dma_offsets_fit(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
+  const int64_t lim = (int64_t)1 << 32;
+  return (M - 1) * lda + K < lim && (N - 1) * ldw + K < lim;
+}
+
+// Tile choice (measured on MI355X): with K % 64 == 0, the 4-wave 256x256 DMA
+// tile once there are enough such tiles to cover the chip, 256x128 for
+// mid-size problems, 128x128 otherwise and whenever M <= 128 (a 256-row tile
+// would compute half its rows for nothing).
+int choose_tile(int64_t M, int64_t N, int64_t K, bool fit) {
+  const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  if (K % 64 == 0 && fit) {
+    if (M <= 128) return kDma128w4;
+    if (t256 >= 192) return kDma256w4;
+    if (t256x128 >= 160) return kDma256x128w4;
+    return kDma128w4;
+  }
+  if (t256 >= 256) return kTile256;
+  if (t128 >= 192) return kTile128;
+  return kTile64x128;
+}
+
+// Split-K when the tiles leave most CUs idle: enough splits to give every CU
+// its full complement of workgroups, each split at least kMinSplitSteps long.
+int choose_ksplit(int64_t tiles, int nk, int per_cu) {
+  const int64_t target = (int64_t)kCUs * per_cu;
+  if (2 * tiles > target) return 1;
+  int64_t s = (target + tiles - 1) / tiles;
+  s = std::min<int64_t>(s, nk / kMinSplitSteps);
+  s = std::min<int64_t>(s, kMaxKSplit);
+  return (int)std::max<int64_t>(s, 1);
+}
+
+}  // namespace
+
+GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
+                   int64_t ws_bytes) {
+  GemmPlan pl{};
+  pl.ksplit = 1;
+  const bool fit = dma_offsets_fit(M, N, K, lda, ldw);
+  pl.tile = tile < 0 ? choose_tile(M, N, K, fit) : tile;
+  if (pl.tile >= kTileCount) return pl.error = "unknown tile", pl;
+  const TileShape sh = shape_of(pl.tile);
+  if (sh.dma && K % 64 != 0) return pl.error = "the pipelined tiles need K % 64 == 0", pl;
+  if (sh.dma && !fit) return pl.error = "the pipelined tiles address each operand with 32-bit offsets", pl;
+  pl.tiles_m = (int)((M + sh.bm - 1) / sh.bm);
+  pl.tiles_n = (int)((N + sh.bn - 1) / sh.bn);
+  const int64_t tiles = (int64_t)pl.tiles_m * pl.tiles_n;
+  const int nk = (int)(K / 64);
+  const int64_t slot = (int64_t)sh.bm * sh.bn * 4;
+  if (ksplit >= 1) {
+    if (ksplit > 1) {
+      if (!sh.dma) return pl.error = "split-K needs a pipelined tile", pl;
+      if (ksplit > kMaxKSplit || ksplit > nk) return pl.error = "ksplit exceeds K / 64 or the split limit", pl;
+      if (tiles * ksplit * slot > ws_bytes) return pl.error = "split-K workspace too small", pl;
+    }
+    pl.ksplit = ksplit;
+  } else if (sh.dma && tiles > 0 && ws_bytes > 0) {
+    const int64_t room = ws_bytes / (tiles * slot);
+    const int s = (int)std::min<int64_t>(choose_ksplit(tiles, nk, sh.per_cu), room);
+    pl.ksplit = s >= 2 ? s : 1;
+  }
+  pl.ws_bytes = pl.ksplit > 1 ? tiles * pl.ksplit * slot : 0;
+  return pl;
+}
+
+hipError_t launch_gemm(int mode, GemmParams p, int epi, int out_dt, const GemmPlan& plan, hipStream_t st) {
   if (p.M == 0 || p.N == 0) return hipSuccess;
-  return mode == kInt8 ? launch_mode<kInt8>(p, epi, out_dt, tile, st) : launch_mode<kFp8>(p, epi, out_dt, tile, st);
+  if (plan.error) return hipErrorInvalidValue;
+  p.ksplit = plan.ksplit;
+  return mode == kInt8 ? launch_mode<kInt8>(p, epi, out_dt, plan.tile, st)
+                       : launch_mode<kFp8>(p, epi, out_dt, plan.tile, st);
 }
 
 }  // namespace d3

@@ -540,6 +540,78 @@ __device__ __forceinline__ void dma16(const uint8_t* gbase, uint32_t voff, uint3
       : "memory", "m0", "scc");
 }
 
+// Split-K, first half: every workgroup of a tile stores its raw accumulators
+// in its own slot of the workspace. Slot layout: 16-byte word (i, j, g) of
+// wave w is 1 KiB of consecutive bytes over the wave's lanes (registers
+// 4g..4g+3 of acc[i][j]), so every store writes whole cache lines.
+template <int NW, int TM, int TN>
+__host__ __device__ constexpr int splitk_wave_words() { return TM * TN * 4 * 64; }
+
+template <int MODE, int NW, int TM, int TN, typename ACC>
+__device__ __forceinline__ void splitk_store(const GemmParams& p, ACC (&acc)[TM][TN], int tile, int split, int wave,
+                                             int lane) {
+  using E = typename std::conditional<MODE == kInt8, int, float>::type;
+  constexpr int WAVE_U4 = splitk_wave_words<NW, TM, TN>(), TILE_U4 = NW * WAVE_U4;
+  uint4* mine = (uint4*)p.partial + ((int64_t)tile * p.ksplit + split) * TILE_U4 + wave * WAVE_U4 + lane;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        mine[((i * TN + j) * 4 + g) * 64] =
+            make_uint4(__builtin_bit_cast(uint32_t, (E)acc[i][j][4 * g]), __builtin_bit_cast(uint32_t, (E)acc[i][j][4 * g + 1]),
+                       __builtin_bit_cast(uint32_t, (E)acc[i][j][4 * g + 2]), __builtin_bit_cast(uint32_t, (E)acc[i][j][4 * g + 3]));
+}
+
+// Split-K, second half (its own launch, so the slots are visible device-wide):
+// one wave per 32-row block of a GEMM wave's sub-tile sums the ksplit slots in
+// split order 0, 1, ..., ksplit-1 (a fixed floating-point order: results do not
+// depend on scheduling) and runs the same epilogue the unsplit kernel runs.
+// Spreading the sum over tiles x NW x TM small workgroups keeps every CU
+// reading instead of one workgroup per tile.
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
+__global__ __launch_bounds__(64) void gemm_splitk_reduce(GemmParams p) {
+  using MF = Mfma<MODE>;
+  typedef typename MF::acc acc_t;
+  using E = typename std::conditional<MODE == kInt8, int, float>::type;
+  constexpr int NW = WM * WN, WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+  constexpr int WAVE_U4 = splitk_wave_words<NW, TM, TN>(), TILE_U4 = NW * WAVE_U4;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[EpiLds<TN, EPI, OUT>::BYTES];
+  const int lane = threadIdx.x;
+  int b = (int)blockIdx.x;
+  const int i = b % TM;
+  b /= TM;
+  const int wave = b % NW;
+  const int tile = b / NW;
+  const int tm = tile / p.tiles_n, tn = tile - (tile / p.tiles_n) * p.tiles_n;
+  const int wm = wave / WN, wn = wave % WN;
+  const int S = p.ksplit;
+  const uint4* src = (const uint4*)p.partial + (int64_t)tile * S * TILE_U4 + wave * WAVE_U4 + i * TN * 4 * 64 + lane;
+  acc_t acc[1][TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[0][j][r] = 0;
+#pragma unroll 2
+  for (int s = 0; s < S; ++s) {
+    uint4 u[TN * 4];
+#pragma unroll
+    for (int w = 0; w < TN * 4; ++w) u[w] = src[(int64_t)s * TILE_U4 + w * 64];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint4 v = u[j * 4 + g];
+        acc[0][j][4 * g] = (E)acc[0][j][4 * g] + __builtin_bit_cast(E, v.x);
+        acc[0][j][4 * g + 1] = (E)acc[0][j][4 * g + 1] + __builtin_bit_cast(E, v.y);
+        acc[0][j][4 * g + 2] = (E)acc[0][j][4 * g + 2] + __builtin_bit_cast(E, v.z);
+        acc[0][j][4 * g + 3] = (E)acc[0][j][4 * g + 3] + __builtin_bit_cast(E, v.w);
+      }
+  }
+  epilogue<MODE, 1, TN, EPI, OUT>(p, acc, (int64_t)tm * BM + wm * WTM + i * 32, (int64_t)tn * BN + wn * WTN, lane, lds);
+}
+
 template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
 __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   using MF = Mfma<MODE>;
@@ -565,16 +637,21 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
+  // ksplit consecutive workgroups share a tile, split s taking K steps [s nk/S, (s+1) nk/S)
+  const int S = p.ksplit;
+  const int split = (int)blockIdx.x % S;
   int tm, tn;
-  tile_of(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
+  tile_of((int)blockIdx.x / S, (int)gridDim.x / S, p.tiles_m, p.tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int nk = (int)(p.K / kBK2);
+  const int nk_all = (int)(p.K / kBK2);
+  const int kbeg = (int)((int64_t)split * nk_all / S);
+  const int nk = (int)((int64_t)(split + 1) * nk_all / S) - kbeg;  // >= 1: the host keeps S <= nk_all
   const int lrow = lane & 31, lhalf = lane >> 5;
 
   // DMA sources: uniform tile bases + per-lane 32-bit offsets (the host keeps every operand
   // offset below 2^32 for this kernel)
-  const uint8_t* a_base = uniform_ptr(p.a + m0 * p.lda);
-  const uint8_t* b_base = uniform_ptr(p.w + n0 * p.ldw);
+  const uint8_t* a_base = uniform_ptr(p.a + m0 * p.lda + (int64_t)kbeg * kBK2);
+  const uint8_t* b_base = uniform_ptr(p.w + n0 * p.ldw + (int64_t)kbeg * kBK2);
   uint32_t a_off[A_DMA], b_off[B_DMA];
 #pragma unroll
   for (int i = 0; i < A_DMA; ++i) {
@@ -721,6 +798,10 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
     if (kt0 + 3 < nk) step(std::integral_constant<int, 3>{}, Checked{}, kt0 + 3);
   }
 
+  if (S > 1) {
+    splitk_store<MODE, NW, TM, TN>(p, acc, tm * p.tiles_n + tn, split, wave, lane);
+    return;
+  }
   // every wave has finished reading the stages before they hold the epilogue's rows
   wait_lgkm0();
   lds_barrier();
@@ -731,17 +812,6 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
 // ---------------------------------------------------------------------------
 // host side: tile-config selection and dispatch
 // ---------------------------------------------------------------------------
-enum TileCfg : int {
-  kTileAuto = -1,
-  kTile256 = 0,      // register-staged 256x256, 4 waves
-  kTile128 = 1,      // register-staged 128x128, 4 waves
-  kTile64x128 = 2,   // register-staged 64x128, 4 waves
-  kDma256w8 = 3,     // DMA pipeline 256x256, 8 waves (128x64 each), 4 stages
-  kDma256w4 = 4,     // DMA pipeline 256x256, 4 waves (128x128 each), 4 stages
-  kDma128w4 = 5,     // DMA pipeline 128x128, 4 waves (64x64 each), 4 stages
-  kDma256x128w4 = 6, // DMA pipeline 256x128, 4 waves (128x64 each), 4 stages
-  kTileCount = 7
-};
 
 template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
 static hipError_t launch_cfg(GemmParams p, hipStream_t st) {
@@ -756,42 +826,22 @@ template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
 static hipError_t launch_dma(GemmParams p, hipStream_t st) {
   p.tiles_m = (int)((p.M + BM - 1) / BM);
   p.tiles_n = (int)((p.N + BN - 1) / BN);
-  const int64_t nb = (int64_t)p.tiles_m * p.tiles_n;
-  hipLaunchKernelGGL((gemm_w8a8_dma<MODE, BM, BN, WM, WN, EPI, OUT>), dim3((unsigned)nb), dim3(WM * WN * 64), 0,
-                     st, p);
-  return hipGetLastError();
-}
-
-// Tile choice (measured on MI355X): the 4-wave 256x256 DMA tile once there are
-// enough such tiles to cover the chip; 256x128 for mid-size problems; 128x128
-// when even that leaves CUs idle.
-static int choose_tile(int64_t M, int64_t N, int64_t K) {
-  const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-  const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
-  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
-  if (K % kBK2 == 0) {
-    if (t256 >= 192) return kDma256w4;
-    if (t256x128 >= 160) return kDma256x128w4;
-    return kDma128w4;
+  const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+  hipLaunchKernelGGL((gemm_w8a8_dma<MODE, BM, BN, WM, WN, EPI, OUT>), dim3((unsigned)(tiles * p.ksplit)),
+                     dim3(WM * WN * 64), 0, st, p);
+  if (p.ksplit > 1) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    constexpr int WAVE_BLOCKS = WM * WN * (BM / WM / 32);  // reduce workgroups per tile
+    hipLaunchKernelGGL((gemm_splitk_reduce<MODE, BM, BN, WM, WN, EPI, OUT>), dim3((unsigned)(tiles * WAVE_BLOCKS)),
+                       dim3(64), 0, st, p);
   }
-  if (t256 >= 256) return kTile256;
-  if (t128 >= 192) return kTile128;
-  return kTile64x128;
-}
-
-// The DMA kernels address operands as a tile base plus a 32-bit per-lane offset.
-static bool dma_offsets_fit(const GemmParams& p) {
-  const int64_t lim = (int64_t)1 << 32;
-  return (p.M - 1) * p.lda + p.K < lim && (p.N - 1) * p.ldw + p.K < lim;
+  return hipGetLastError();
 }
 
 template <int MODE, int EPI, int OUT>
 hipError_t launch_epi(GemmParams p, int tile, hipStream_t st) {
-  if (tile == kTileAuto) {
-    tile = choose_tile(p.M, p.N, p.K);
-    if (tile >= kDma256w8 && !dma_offsets_fit(p)) tile = tile == kDma256w4 ? kTile256 : kTile128;
-  }
-  if (tile >= kDma256w8 && (p.K % kBK2 != 0 || !dma_offsets_fit(p))) return hipErrorInvalidValue;
+  if (p.ksplit < 1 || (p.ksplit > 1 && tile < kDma256w8)) return hipErrorInvalidValue;
   switch (tile) {
     case kTile256: return launch_cfg<MODE, 256, 256, 2, 2, EPI, OUT>(p, st);
     case kTile128: return launch_cfg<MODE, 128, 128, 2, 2, EPI, OUT>(p, st);

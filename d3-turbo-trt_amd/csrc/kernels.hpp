@@ -22,6 +22,12 @@ struct GemmParams {
   const int32_t* row_map;
   int vec;  // output, residual and channel scales allow 4-element vector access
   int tiles_m, tiles_n;
+  // Split-K (pipelined tiles only): ksplit workgroups share one output tile,
+  // each over a contiguous range of K steps, and store their raw accumulators
+  // in `partial` (ksplit tile-sized slots per tile); a second launch sums the
+  // slots in split order and runs the epilogue.
+  int ksplit;
+  uint32_t* partial;  // tiles * ksplit * BM * BN 32-bit words
 };
 
 hipError_t launch_quant_rows(int mode, int dt, const void* x, int64_t ldx, int64_t M, int64_t K, void* q,
@@ -41,7 +47,32 @@ struct SegOffsets {
 hipError_t launch_quant_ragged(int mode, int dt, int out_es, const void* x, int64_t ldx, const SegOffsets& segs,
                                int64_t nseg, int64_t width, int64_t K, void* q, int64_t ldq, float* scale,
                                int32_t* row_map, void* out, int64_t ldo, int64_t N, hipStream_t st);
-hipError_t launch_gemm(int mode, GemmParams p, int epi, int out_dt, int tile, hipStream_t st);
+enum TileCfg : int {
+  kTileAuto = -1,
+  kTile256 = 0,      // register-staged 256x256, 4 waves
+  kTile128 = 1,      // register-staged 128x128, 4 waves
+  kTile64x128 = 2,   // register-staged 64x128, 4 waves
+  kDma256w8 = 3,     // DMA pipeline 256x256, 8 waves (128x64 each), 4 stages
+  kDma256w4 = 4,     // DMA pipeline 256x256, 4 waves (128x128 each), 4 stages
+  kDma128w4 = 5,     // DMA pipeline 128x128, 4 waves (64x64 each), 4 stages
+  kDma256x128w4 = 6, // DMA pipeline 256x128, 4 waves (128x64 each), 4 stages
+  kTileCount = 7
+};
+
+constexpr int kMaxKSplit = 32;
+
+// Tile and split-K choice for one GEMM. `tile` / `ksplit` < 0 ask for the
+// automatic choice; a workspace of `ws_bytes` (0: none) bounds ksplit.
+struct GemmPlan {
+  int tile, ksplit;
+  int tiles_m, tiles_n;
+  int64_t ws_bytes;  // workspace the plan uses (0 when ksplit == 1)
+  const char* error; // non-null: the request is not valid
+};
+GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
+                   int64_t ws_bytes);
+// Launches the plan; p.partial must point to a workspace of plan.ws_bytes.
+hipError_t launch_gemm(int mode, GemmParams p, int epi, int out_dt, const GemmPlan& plan, hipStream_t st);
 
 constexpr int64_t kMaxVecK = 32 * 512;  // longest row the one-pass quant kernels hold in registers
 

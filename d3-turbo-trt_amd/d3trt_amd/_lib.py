@@ -20,6 +20,7 @@ BF16, F16, F32 = 0, 1, 2
 EPI_DEQUANT, EPI_RAW, EPI_SWIGLU, EPI_RESIDUAL = 0, 1, 2, 3
 TILE_AUTO, TILE_256, TILE_128, TILE_64x128 = -1, 0, 1, 2
 MAX_SEGMENTS = 256  # D3W8A8_MAX_SEGMENTS: blocks of one ragged batch
+KSPLIT_AUTO = -1  # D3W8A8_KSPLIT_AUTO
 TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4 = 3, 4, 5, 6
 TILES = (TILE_256, TILE_128, TILE_64x128, TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4)
 DMA_TILES = (TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4)
@@ -39,6 +40,12 @@ SIGNATURES = {
                                     _i64, _i64, _p],
     "d3w8a8_gemm": [_i32, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p, _i64, _p,
                     _p, _i32, _p],
+    "d3w8a8_gemm_ws": [_i32, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p, _i64, _p,
+                       _p, _i32, _i32, _p, _i64, _p],
+}
+# name -> argtypes of the entry points that return int64
+INT64_FUNCS = {
+    "d3w8a8_gemm_workspace": [_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i64],
 }
 STRING_FUNCS = ("d3w8a8_version", "d3w8a8_last_error")
 
@@ -70,6 +77,10 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes
                 fn.restype = ctypes.c_int
+            for name, argtypes in INT64_FUNCS.items():
+                fn = getattr(lib, name)
+                fn.argtypes = argtypes
+                fn.restype = ctypes.c_int64
             for name in STRING_FUNCS:
                 fn = getattr(lib, name)
                 fn.argtypes = []

@@ -156,8 +156,14 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
          w_scale: Optional[torch.Tensor], *, epilogue: int = _lib.EPI_DEQUANT,
          out_dtype: torch.dtype = torch.bfloat16, out: Optional[torch.Tensor] = None,
          residual: Optional[torch.Tensor] = None, row_amax: Optional[torch.Tensor] = None,
-         row_map: Optional[torch.Tensor] = None, tile: int = _lib.TILE_AUTO) -> torch.Tensor:
-    """W8A8 GEMM ``a @ w.T`` with a fused epilogue (see include/d3w8a8.h)."""
+         row_map: Optional[torch.Tensor] = None, tile: int = _lib.TILE_AUTO,
+         ksplit: int = _lib.KSPLIT_AUTO) -> torch.Tensor:
+    """W8A8 GEMM ``a @ w.T`` with a fused epilogue (see include/d3w8a8.h).
+
+    Skinny problems may split K over several workgroups per output tile
+    (``ksplit``, automatic by default); the split-K workspace is this module's
+    per-(device, stream) buffer from :func:`workspace`.
+    """
     a = _rows(a, "a")
     w = _rows(w, "w")
     M, K = a.shape
@@ -202,13 +208,38 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
         if a_scale is None or w_scale is None or a_scale.numel() != M or w_scale.numel() != N:
             raise ValueError("dequantizing epilogues need a_scale [M] and w_scale [N]")
     lib = _lib.load()
-    rc = lib.d3w8a8_gemm(
+    st = _stream(a)
+    ws = workspace(a.device, st) if ksplit != 1 else None
+    rc = lib.d3w8a8_gemm_ws(
         mode_code(mode), a.data_ptr(), a.stride(0), _ptr(a_scale), w.data_ptr(), w.stride(0), _ptr(w_scale),
         M, N, K, epilogue, dtype_code(odt) if epilogue != _lib.EPI_RAW else 0, out.data_ptr(), out.stride(0),
         _ptr(residual), residual.stride(0) if residual is not None else 0, _ptr(row_amax), _ptr(row_map),
-        tile, _stream(a))
+        tile, ksplit, _ptr(ws), ws.numel() if ws is not None else 0, st)
     _lib.check(rc, "gemm")
     return out
+
+
+WORKSPACE_BYTES = 64 << 20
+_workspaces: dict = {}
+
+
+def workspace(device: torch.device, stream: int) -> torch.Tensor:
+    """The split-K workspace of one (device, stream): WORKSPACE_BYTES of device memory.
+
+    GEMMs on one stream run in order, so they can share it. The first GEMM on
+    a stream must not be inside a graph capture (the allocation would be
+    captured); warm the stream up eagerly.
+    """
+    device = torch.device(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _workspaces.get(key)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("the first GEMM on a stream runs eagerly (it allocates the split-K workspace); "
+                               "warm the stream up before capturing a graph on it")
+        ws = torch.empty(WORKSPACE_BYTES, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
 
 
 def interleave_gate_up(full: torch.Tensor) -> torch.Tensor:

@@ -163,11 +163,11 @@ class GraphedStack:
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
-            for _ in range(2):  # warm the allocator outside the capture
+            for _ in range(2):  # warm the allocator (and the stream's split-K workspace) outside the capture
                 stack.forward(self.static_in)
         torch.cuda.current_stream(dev).wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        with torch.cuda.graph(self.graph, stream=side):
             self.static_out = stack.forward(self.static_in)
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:

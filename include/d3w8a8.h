@@ -113,6 +113,31 @@ int d3w8a8_gemm(int mode, const void* a, int64_t lda, const float* a_scale, cons
                 int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
                 void* stream);
 
+/* d3w8a8_gemm with a caller-owned workspace that lets skinny problems split K.
+ * Same operation, arguments and results as d3w8a8_gemm (the reference's
+ * question passes, backends/trtllm.py:149-179, run every projection at a small
+ * M; with too few output tiles to occupy the GPU, `ksplit` workgroups share
+ * each tile over disjoint K ranges). The partial sums are added in a fixed
+ * order (a second launch reads them), so results do not depend on
+ * scheduling: INT8 equals d3w8a8_gemm bit for bit; FP8 differs from it only
+ * by fp32 summation order.
+ *   ksplit: D3W8A8_KSPLIT_AUTO (chosen from the shape and the workspace size),
+ *           or 1..32 (>1 needs a DMA tile and K / 64 >= ksplit).
+ *   workspace: device memory, 256-byte aligned, `workspace_bytes` long, of
+ *           any contents (it holds partial sums between the two launches).
+ *           Calls that share a workspace must be ordered (same stream);
+ *           NULL / 0 means no split. */
+#define D3W8A8_KSPLIT_AUTO (-1)
+int d3w8a8_gemm_ws(int mode, const void* a, int64_t lda, const float* a_scale, const void* w, int64_t ldw,
+                   const float* w_scale, int64_t M, int64_t N, int64_t K, int epilogue, int out_dtype, void* out,
+                   int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
+                   int ksplit, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes d3w8a8_gemm_ws uses for this problem, tile and ksplit when
+ * given at most `max_bytes` (0 when it would not split); -1 on bad arguments. */
+int64_t d3w8a8_gemm_workspace(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
+                              int64_t max_bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -84,7 +84,7 @@ def _header_functions():
 def test_library_exports_every_header_symbol():
     lib = _lib.load()
     names = _header_functions()
-    assert set(names) == set(_lib.SIGNATURES) | set(_lib.STRING_FUNCS)
+    assert set(names) == set(_lib.SIGNATURES) | set(_lib.STRING_FUNCS) | set(_lib.INT64_FUNCS)
     for name in names:
         assert hasattr(lib, name), name
     assert "gfx950" in _lib.version()
@@ -133,3 +133,34 @@ def test_ragged_lengths_are_checked_on_the_host():
                                            dummy, None, 0, 0, 0, None) == _lib.EINVAL
     header = open(os.path.join(ROOT, "include", "d3w8a8.h")).read()
     assert re.search(r"#define D3W8A8_MAX_SEGMENTS (\d+)", header).group(1) == str(_lib.MAX_SEGMENTS)
+
+
+def test_split_k_plan_on_the_host():
+    """Workspace sizing and split-K validation run on the host (no launch)."""
+    lib = _lib.load()
+    big = 64 << 20
+    slot = 128 * 128 * 4
+    # 128 rows x 4096 columns: 32 tiles of 128x128 leave the GPU idle -> 16 splits of 4 K steps each
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, big) == \
+        32 * 16 * slot
+    # a smaller workspace lowers the automatic split; none at all means no split
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1,
+                                     32 * 5 * slot) == \
+        32 * 5 * slot
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, 0) == 0
+    # state-pass shapes fill the GPU without splitting
+    assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, -1, -1, big) == 0
+    # explicit requests are checked, not adjusted
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, 5, 4, big) == \
+        32 * 4 * slot
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 256, 256, 256, 5, 8, big) == -1   # 4 K steps < 8 splits
+    assert b"ksplit" in lib.d3w8a8_last_error()
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, 5, 4, 1 << 20) == -1
+    assert b"too small" in lib.d3w8a8_last_error()
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, 1, 2, big) == -1  # register-staged tile
+    assert b"pipelined" in lib.d3w8a8_last_error()
+    dummy = 256
+    assert lib.d3w8a8_gemm_ws(0, dummy, 4096, dummy, dummy, 4096, dummy, 128, 4096, 4096, 0, 0, dummy, 4096,
+                              None, 0, None, None, 5, 4, dummy, 1 << 20, None) == _lib.EINVAL
+    header = open(os.path.join(ROOT, "include", "d3w8a8.h")).read()
+    assert re.search(r"#define D3W8A8_KSPLIT_AUTO \((-?\d+)\)", header).group(1) == str(_lib.KSPLIT_AUTO)
