@@ -136,7 +136,7 @@ static int gemm_impl(int mode, const void* a, int64_t lda, const float* a_scale,
   if (epilogue < D3W8A8_EPI_DEQUANT || epilogue > D3W8A8_EPI_RESIDUAL)
     return fail(D3W8A8_EINVAL, "gemm: unknown epilogue %d", epilogue);
   if (epilogue != D3W8A8_EPI_RAW && !dtype_ok(out_dtype)) return fail(D3W8A8_EINVAL, "gemm: unknown out dtype");
-  if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_256x128_W4) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
+  if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_128_W4_K128) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
   if (ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) return fail(D3W8A8_EINVAL, "gemm: bad ksplit %d", ksplit);
   if (workspace_bytes < 0 || (workspace_bytes > 0 && (!workspace || !aligned(workspace, 256))))
     return fail(D3W8A8_EINVAL, "gemm: the workspace must be 256-byte aligned device memory");
@@ -191,7 +191,7 @@ int d3w8a8_gemm_ws(int mode, const void* a, int64_t lda, const float* a_scale, c
 int64_t d3w8a8_gemm_workspace(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
                               int64_t max_bytes) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 16 || lda < K || ldw < K || M > INT32_MAX / 2 || N > INT32_MAX / 2 ||
-      tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_256x128_W4 || ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) {
+      tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_128_W4_K128 || ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) {
     fail(D3W8A8_EINVAL, "gemm_workspace: bad arguments");
     return -1;
   }

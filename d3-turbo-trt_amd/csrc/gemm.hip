@@ -51,24 +51,25 @@ namespace {
 struct TileShape {
   int bm, bn;
   bool dma;
-  int per_cu;  // workgroups one CU holds at once (LDS: 4 stages of (bm + bn) x 64 bytes)
+  int bk;      // bytes of K per pipeline step (K must be a multiple)
 };
 
 TileShape shape_of(int tile) {
   switch (tile) {
-    case kTile256: return {256, 256, false, 1};
-    case kTile128: return {128, 128, false, 1};
-    case kTile64x128: return {64, 128, false, 1};
-    case kDma256w8: return {256, 256, true, 1};
-    case kDma256w4: return {256, 256, true, 1};
-    case kDma128w4: return {128, 128, true, 2};
-    case kDma256x128w4: return {256, 128, true, 1};
+    case kTile256: return {256, 256, false, 16};
+    case kTile128: return {128, 128, false, 16};
+    case kTile64x128: return {64, 128, false, 16};
+    case kDma256w8: return {256, 256, true, 64};
+    case kDma256w4: return {256, 256, true, 64};
+    case kDma128w4: return {128, 128, true, 64};
+    case kDma256x128w4: return {256, 128, true, 64};
+    case kDma128w4k128: return {128, 128, true, 128};
   }
   return {0, 0, false, 0};
 }
 
-constexpr int kCUs = 256;          // MI355X compute units
-constexpr int kMinSplitSteps = 4;  // K steps (64 bytes each) per split at least
+constexpr int kCUs = 256;              // MI355X compute units
+constexpr int kMinSplitBytes = 1024;   // bytes of K per split at least
 
 // The DMA kernels address operands as a tile base plus a 32-bit per-lane offset.
 bool dma_offsets_fit(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
@@ -78,14 +79,15 @@ bool dma_offsets_fit(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) 
 
 // Tile choice (measured on MI355X): with K % 64 == 0, the 4-wave 256x256 DMA
 // tile once there are enough such tiles to cover the chip, 256x128 for
-// mid-size problems, 128x128 otherwise and whenever M <= 128 (a 256-row tile
-// would compute half its rows for nothing).
+// mid-size problems, 128x128 otherwise. M <= 128 (a 256-row tile would compute
+// half its rows for nothing) streams the weights: 128x128 with 128-byte K
+// steps when K allows.
 int choose_tile(int64_t M, int64_t N, int64_t K, bool fit) {
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
   if (K % 64 == 0 && fit) {
-    if (M <= 128) return kDma128w4;
+    if (M <= 128) return K % 128 == 0 ? kDma128w4k128 : kDma128w4;
     if (t256 >= 192) return kDma256w4;
     if (t256x128 >= 160) return kDma256x128w4;
     return kDma128w4;
@@ -95,13 +97,15 @@ int choose_tile(int64_t M, int64_t N, int64_t K, bool fit) {
   return kTile64x128;
 }
 
-// Split-K when the tiles leave most CUs idle: enough splits to give every CU
-// its full complement of workgroups, each split at least kMinSplitSteps long.
-int choose_ksplit(int64_t tiles, int nk, int per_cu) {
-  const int64_t target = (int64_t)kCUs * per_cu;
+// Split-K when the tiles leave most CUs idle: about one workgroup per CU,
+// each split at least kMinSplitBytes of K. Measured on MI355X at M = 128
+// (weights streamed from HBM): more splits cost more in partial sums and the
+// reduce launch than the extra workgroups gain.
+int choose_ksplit(int64_t tiles, int nk, int bk) {
+  const int64_t target = kCUs;
   if (2 * tiles > target) return 1;
   int64_t s = (target + tiles - 1) / tiles;
-  s = std::min<int64_t>(s, nk / kMinSplitSteps);
+  s = std::min<int64_t>(s, nk / (kMinSplitBytes / bk));
   s = std::min<int64_t>(s, kMaxKSplit);
   return (int)std::max<int64_t>(s, 1);
 }
@@ -116,23 +120,25 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, in
   pl.tile = tile < 0 ? choose_tile(M, N, K, fit) : tile;
   if (pl.tile >= kTileCount) return pl.error = "unknown tile", pl;
   const TileShape sh = shape_of(pl.tile);
-  if (sh.dma && K % 64 != 0) return pl.error = "the pipelined tiles need K % 64 == 0", pl;
+  if (sh.dma && K % sh.bk != 0)
+    return pl.error = sh.bk == 128 ? "the 128-byte-step tile needs K % 128 == 0" : "the pipelined tiles need K % 64 == 0",
+           pl;
   if (sh.dma && !fit) return pl.error = "the pipelined tiles address each operand with 32-bit offsets", pl;
   pl.tiles_m = (int)((M + sh.bm - 1) / sh.bm);
   pl.tiles_n = (int)((N + sh.bn - 1) / sh.bn);
   const int64_t tiles = (int64_t)pl.tiles_m * pl.tiles_n;
-  const int nk = (int)(K / 64);
+  const int nk = (int)(K / (sh.dma ? sh.bk : 64));
   const int64_t slot = (int64_t)sh.bm * sh.bn * 4;
   if (ksplit >= 1) {
     if (ksplit > 1) {
-      if (!sh.dma) return pl.error = "split-K needs a pipelined tile", pl;
+      if (!sh.dma || sh.bm != 128 || sh.bn != 128) return pl.error = "split-K needs a pipelined 128x128 tile", pl;
       if (ksplit > kMaxKSplit || ksplit > nk) return pl.error = "ksplit exceeds K / 64 or the split limit", pl;
       if (tiles * ksplit * slot > ws_bytes) return pl.error = "split-K workspace too small", pl;
     }
     pl.ksplit = ksplit;
-  } else if (sh.dma && tiles > 0 && ws_bytes > 0) {
+  } else if (sh.dma && sh.bm == 128 && sh.bn == 128 && tiles > 0 && ws_bytes > 0) {
     const int64_t room = ws_bytes / (tiles * slot);
-    const int s = (int)std::min<int64_t>(choose_ksplit(tiles, nk, sh.per_cu), room);
+    const int s = (int)std::min<int64_t>(choose_ksplit(tiles, nk, sh.bk), room);
     pl.ksplit = s >= 2 ? s : 1;
   }
   pl.ws_bytes = pl.ksplit > 1 ? tiles * pl.ksplit * slot : 0;

@@ -456,15 +456,19 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8(GemmParams p) {
 
 
 // ---------------------------------------------------------------------------
-// Pipelined kernel (K % 64 == 0): 64-byte K steps, 4 LDS stages filled by
-// direct global->LDS DMA (global_load_lds_dwordx4), one barrier per step.
+// Pipelined kernel (K % BK == 0): BK-byte K steps (64, or 128 for the
+// weight-streaming tile), 4 LDS stages filled by direct global->LDS DMA
+// (global_load_lds_dwordx4), one barrier per step.
 //
 //   * DMA: each instruction of a wave writes 1 KiB of LDS (64 lanes x 16 B):
-//     16 rows of 64 bytes. Lane j carries row r0 + j/4 and physical chunk
-//     j%4, i.e. logical K chunk (j%4) ^ ((row >> 2) & 3): the XOR swizzle that
-//     makes the MFMA operand reads (one 16-byte chunk of 32 consecutive rows)
-//     conflict-free (a ds_read_b128 serves 16 lanes per cycle from 64 banks).
-//     Sources are a uniform base (SGPRs, advanced by 64 bytes per step) plus
+//     1024/BK rows of BK bytes. Lane j carries row r0 + j/(BK/16) and physical
+//     chunk j%(BK/16), i.e. logical K chunk (j%(BK/16)) ^ swz(row): the XOR
+//     swizzle that makes the MFMA operand reads (one 16-byte chunk of 32
+//     consecutive rows) conflict-free (a ds_read_b128 serves 16 lanes per
+//     cycle from 64 banks). 128-byte steps fetch whole 128-byte lines of each
+//     row, which HBM streams at ~6 TB/s where 64-byte pieces of many rows
+//     reach ~4 TB/s (measured on MI355X): the skinny-M tile uses them.
+//     Sources are a uniform base (SGPRs, advanced by BK bytes per step) plus
 //     a 32-bit per-lane offset; the LDS address is this wave's slot in stage
 //     0 plus a compile-time stage/row offset. Rows past M (or N) are clamped
 //     to the last row: they only feed output rows (columns) never stored.
@@ -481,12 +485,18 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8(GemmParams p) {
 //   * Steps with a full pipeline ahead run unchecked; the last steps of the
 //     K loop (CHECKED) guard the reads and DMAs that would pass the end.
 // ---------------------------------------------------------------------------
-constexpr int kBK2 = 64;
 constexpr int kStages = 4;
 
-// 64-byte rows: the 16 lanes of one ds_read_b128 cycle read rows r..r+15 (four rows per 256-byte bank
-// line); XOR-ing the chunk with (row >> 2) & 3 spreads them over the 16 bank groups.
-__device__ __forceinline__ int lds_off64(int row, int chunk) { return row * kBK2 + ((chunk ^ ((row >> 2) & 3)) << 4); }
+// LDS swizzle of BK-byte rows. 64-byte rows: the 16 lanes of one ds_read_b128 cycle read rows
+// r..r+15 (four rows per 256-byte bank line); XOR-ing the chunk with (row >> 2) & 3 spreads them over
+// the 16 bank groups. 128-byte rows: two rows per bank line; XOR with (row >> 1) & 7.
+template <int BK>
+__host__ __device__ __forceinline__ int lds_swz(int row) {
+  static_assert(BK == 64 || BK == 128, "step bytes");
+  return BK == 64 ? (row >> 2) & 3 : (row >> 1) & 7;
+}
+template <int BK>
+__device__ __forceinline__ int lds_offk(int row, int chunk) { return row * BK + ((chunk ^ lds_swz<BK>(row)) << 4); }
 
 // s_barrier without the fence __syncthreads() adds (whose vmcnt(0) would drain
 // the DMA pipeline); the empty asm keeps the compiler from moving LDS accesses
@@ -546,6 +556,10 @@ __device__ __forceinline__ void dma16(const uint8_t* gbase, uint32_t voff, uint3
 // 4g..4g+3 of acc[i][j]), so every store writes whole cache lines.
 template <int NW, int TM, int TN>
 __host__ __device__ constexpr int splitk_wave_words() { return TM * TN * 4 * 64; }
+
+// Tiles that carry the split-K path.
+template <int BM, int BN>
+constexpr bool kSplitTile = BM == 128 && BN == 128;
 
 template <int MODE, int NW, int TM, int TN, typename ACC>
 __device__ __forceinline__ void splitk_store(const GemmParams& p, ACC (&acc)[TM][TN], int tile, int split, int wave,
@@ -612,7 +626,7 @@ __global__ __launch_bounds__(64) void gemm_splitk_reduce(GemmParams p) {
   epilogue<MODE, 1, TN, EPI, OUT>(p, acc, (int64_t)tm * BM + wm * WTM + i * 32, (int64_t)tn * BN + wn * WTN, lane, lds);
 }
 
-template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT, int BK>
 __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   using MF = Mfma<MODE>;
   typedef typename MF::frag frag_t;
@@ -620,10 +634,11 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int A_BYTES = BM * kBK2, B_BYTES = BN * kBK2, STAGE = A_BYTES + B_BYTES;
+  constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK, STAGE = A_BYTES + B_BYTES;
   constexpr int A_DMA = A_BYTES / (1024 * NW), B_DMA = B_BYTES / (1024 * NW);
   constexpr int DPS = A_DMA + B_DMA;            // DMA instructions per wave per step
-  constexpr int SUB = MODE == kInt8 ? 2 : 1;    // MFMAs along K per 64-byte step
+  constexpr int CPR = BK / 16, RPD = 64 / CPR;  // 16-byte chunks per row, rows per DMA instruction
+  constexpr int SUB = MODE == kInt8 ? BK / 32 : BK / 64;  // MFMAs along K per step
   constexpr int FW = MODE == kInt8 ? 1 : 2;     // 16-byte LDS words per MFMA operand
   constexpr int NMF = SUB * TM * TN;            // MFMAs per step
   constexpr int PRE = NMF >= 4 ? 2 : 1;         // MFMAs issued before the barrier
@@ -637,32 +652,36 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
-  // ksplit consecutive workgroups share a tile, split s taking K steps [s nk/S, (s+1) nk/S)
-  const int S = p.ksplit;
-  const int split = (int)blockIdx.x % S;
+  // ksplit consecutive workgroups share a tile, split s taking K steps [s nk/S, (s+1) nk/S).
+  // Only the 128x128 tiles carry the split path (the 256-row tiles hold too many accumulators to
+  // add it without spilling).
+  const int S = kSplitTile<BM, BN> ? p.ksplit : 1;
+  const int split = kSplitTile<BM, BN> ? (int)blockIdx.x % S : 0;
   int tm, tn;
-  tile_of((int)blockIdx.x / S, (int)gridDim.x / S, p.tiles_m, p.tiles_n, tm, tn);
+  if constexpr (kSplitTile<BM, BN>) tile_of((int)blockIdx.x / S, (int)gridDim.x / S, p.tiles_m, p.tiles_n, tm, tn);
+  else tile_of(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int nk_all = (int)(p.K / kBK2);
-  const int kbeg = (int)((int64_t)split * nk_all / S);
-  const int nk = (int)((int64_t)(split + 1) * nk_all / S) - kbeg;  // >= 1: the host keeps S <= nk_all
+  const int nk_all = (int)(p.K / BK);
+  const int kbeg = kSplitTile<BM, BN> ? (int)((int64_t)split * nk_all / S) : 0;
+  // >= 1: the host keeps S <= nk_all
+  const int nk = kSplitTile<BM, BN> ? (int)((int64_t)(split + 1) * nk_all / S) - kbeg : nk_all;
   const int lrow = lane & 31, lhalf = lane >> 5;
 
   // DMA sources: uniform tile bases + per-lane 32-bit offsets (the host keeps every operand
   // offset below 2^32 for this kernel)
-  const uint8_t* a_base = uniform_ptr(p.a + m0 * p.lda + (int64_t)kbeg * kBK2);
-  const uint8_t* b_base = uniform_ptr(p.w + n0 * p.ldw + (int64_t)kbeg * kBK2);
+  const uint8_t* a_base = uniform_ptr(p.a + m0 * p.lda + (int64_t)kbeg * BK);
+  const uint8_t* b_base = uniform_ptr(p.w + n0 * p.ldw + (int64_t)kbeg * BK);
   uint32_t a_off[A_DMA], b_off[B_DMA];
 #pragma unroll
   for (int i = 0; i < A_DMA; ++i) {
-    const int row = (i * NW + wave) * 16 + (lane >> 2);
-    const int ch = (lane & 3) ^ ((row >> 2) & 3);
+    const int row = (i * NW + wave) * RPD + lane / CPR;
+    const int ch = (lane % CPR) ^ lds_swz<BK>(row);
     a_off[i] = (uint32_t)((min(m0 + row, p.M - 1) - m0) * p.lda + ch * 16);
   }
 #pragma unroll
   for (int i = 0; i < B_DMA; ++i) {
-    const int row = (i * NW + wave) * 16 + (lane >> 2);
-    const int ch = (lane & 3) ^ ((row >> 2) & 3);
+    const int row = (i * NW + wave) * RPD + lane / CPR;
+    const int ch = (lane % CPR) ^ lds_swz<BK>(row);
     b_off[i] = (uint32_t)((min(n0 + row, p.N - 1) - n0) * p.ldw + ch * 16);
   }
   const uint32_t lds_wave =
@@ -671,7 +690,7 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   // DMA d of step kt into stage U
   auto dma_one = [&](auto u_c, auto d_c, int kt) {
     constexpr int U = decltype(u_c)::value % kStages, d = decltype(d_c)::value;
-    const int64_t kb = (int64_t)kt * kBK2;
+    const int64_t kb = (int64_t)kt * BK;
     if constexpr (d < A_DMA) dma16<U * STAGE + d * NW * 1024>(a_base + kb, a_off[d], lds_wave);
     else dma16<U * STAGE + A_BYTES + (d - A_DMA) * NW * 1024>(b_base + kb, b_off[d - A_DMA], lds_wave);
   };
@@ -692,8 +711,8 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   auto read_a = [&](auto u_c, auto s_c, auto i_c, auto h_c) {
     constexpr int U = decltype(u_c)::value % kStages, s = decltype(s_c)::value;
     constexpr int i = decltype(i_c)::value, h = decltype(h_c)::value;
-    const int chunk = MODE == kInt8 ? 2 * s + lhalf : 2 * lhalf + h;
-    const v4i v = *(const v4i*)(lds + U * STAGE + lds_off64(wm * WTM + i * 32 + lrow, chunk));
+    const int chunk = MODE == kInt8 ? 2 * s + lhalf : 4 * s + 2 * lhalf + h;
+    const v4i v = *(const v4i*)(lds + U * STAGE + lds_offk<BK>(wm * WTM + i * 32 + lrow, chunk));
     if constexpr (MODE == kInt8) fa[s][i] = v;
     else if constexpr (h == 0) fa[s][i].lo = v;
     else fa[s][i].hi = v;
@@ -701,8 +720,8 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   auto read_b = [&](auto u_c, auto p_c, auto w_c) {
     constexpr int U = decltype(u_c)::value % kStages, P = decltype(p_c)::value, w = decltype(w_c)::value;
     constexpr int s = w / (TN * FW), j = (w / FW) % TN, h = w % FW;
-    const int chunk = MODE == kInt8 ? 2 * s + lhalf : 2 * lhalf + h;
-    const v4i v = *(const v4i*)(lds + U * STAGE + A_BYTES + lds_off64(wn * WTN + j * 32 + lrow, chunk));
+    const int chunk = MODE == kInt8 ? 2 * s + lhalf : 4 * s + 2 * lhalf + h;
+    const v4i v = *(const v4i*)(lds + U * STAGE + A_BYTES + lds_offk<BK>(wn * WTN + j * 32 + lrow, chunk));
     if constexpr (MODE == kInt8) fb[P][s][j] = v;
     else if constexpr (h == 0) fb[P][s][j].lo = v;
     else fb[P][s][j].hi = v;
@@ -798,9 +817,11 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
     if (kt0 + 3 < nk) step(std::integral_constant<int, 3>{}, Checked{}, kt0 + 3);
   }
 
-  if (S > 1) {
-    splitk_store<MODE, NW, TM, TN>(p, acc, tm * p.tiles_n + tn, split, wave, lane);
-    return;
+  if constexpr (kSplitTile<BM, BN>) {
+    if (S > 1) {
+      splitk_store<MODE, NW, TM, TN>(p, acc, tm * p.tiles_n + tn, split, wave, lane);
+      return;
+    }
   }
   // every wave has finished reading the stages before they hold the epilogue's rows
   wait_lgkm0();
@@ -822,14 +843,14 @@ static hipError_t launch_cfg(GemmParams p, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT, int BK = 64>
 static hipError_t launch_dma(GemmParams p, hipStream_t st) {
   p.tiles_m = (int)((p.M + BM - 1) / BM);
   p.tiles_n = (int)((p.N + BN - 1) / BN);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
-  hipLaunchKernelGGL((gemm_w8a8_dma<MODE, BM, BN, WM, WN, EPI, OUT>), dim3((unsigned)(tiles * p.ksplit)),
+  hipLaunchKernelGGL((gemm_w8a8_dma<MODE, BM, BN, WM, WN, EPI, OUT, BK>), dim3((unsigned)(tiles * p.ksplit)),
                      dim3(WM * WN * 64), 0, st, p);
-  if (p.ksplit > 1) {
+  if (kSplitTile<BM, BN> && p.ksplit > 1) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     constexpr int WAVE_BLOCKS = WM * WN * (BM / WM / 32);  // reduce workgroups per tile
@@ -850,6 +871,7 @@ hipError_t launch_epi(GemmParams p, int tile, hipStream_t st) {
     case kDma256w4: return launch_dma<MODE, 256, 256, 2, 2, EPI, OUT>(p, st);
     case kDma128w4: return launch_dma<MODE, 128, 128, 2, 2, EPI, OUT>(p, st);
     case kDma256x128w4: return launch_dma<MODE, 256, 128, 2, 2, EPI, OUT>(p, st);
+    case kDma128w4k128: return launch_dma<MODE, 128, 128, 2, 2, EPI, OUT, 128>(p, st);
   }
   return hipErrorInvalidValue;
 }

@@ -56,7 +56,8 @@ enum TileCfg : int {
   kDma256w4 = 4,     // DMA pipeline 256x256, 4 waves (128x128 each), 4 stages
   kDma128w4 = 5,     // DMA pipeline 128x128, 4 waves (64x64 each), 4 stages
   kDma256x128w4 = 6, // DMA pipeline 256x128, 4 waves (128x64 each), 4 stages
-  kTileCount = 7
+  kDma128w4k128 = 7, // DMA pipeline 128x128, 4 waves, 128-byte K steps (weight streaming, K % 128 == 0)
+  kTileCount = 8
 };
 
 constexpr int kMaxKSplit = 32;

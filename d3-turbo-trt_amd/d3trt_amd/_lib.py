@@ -22,8 +22,15 @@ TILE_AUTO, TILE_256, TILE_128, TILE_64x128 = -1, 0, 1, 2
 MAX_SEGMENTS = 256  # D3W8A8_MAX_SEGMENTS: blocks of one ragged batch
 KSPLIT_AUTO = -1  # D3W8A8_KSPLIT_AUTO
 TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4 = 3, 4, 5, 6
-TILES = (TILE_256, TILE_128, TILE_64x128, TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4)
-DMA_TILES = (TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4)
+TILE_DMA_128_W4_K128 = 7  # 128-byte K steps: K % 128 == 0
+TILES = (TILE_256, TILE_128, TILE_64x128, TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4,
+         TILE_DMA_128_W4_K128)
+DMA_TILES = (TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4, TILE_DMA_128_W4_K128)
+
+
+def tile_k_multiple(tile: int) -> int:
+    """K must be a multiple of this for `tile` (16 for the register-staged tiles)."""
+    return 128 if tile == TILE_DMA_128_W4_K128 else 64 if tile in DMA_TILES else 16
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64

@@ -58,6 +58,7 @@ extern "C" {
 #define D3W8A8_TILE_DMA_256_W4 4    /* DMA 256x256, 4 waves */
 #define D3W8A8_TILE_DMA_128_W4 5    /* DMA 128x128, 4 waves */
 #define D3W8A8_TILE_DMA_256x128_W4 6 /* DMA 256x128, 4 waves */
+#define D3W8A8_TILE_DMA_128_W4_K128 7 /* DMA 128x128, 4 waves, 128-byte K steps (K % 128 == 0): weight streaming */
 
 const char* d3w8a8_version(void);
 const char* d3w8a8_last_error(void);
@@ -122,7 +123,8 @@ int d3w8a8_gemm(int mode, const void* a, int64_t lda, const float* a_scale, cons
  * scheduling: INT8 equals d3w8a8_gemm bit for bit; FP8 differs from it only
  * by fp32 summation order.
  *   ksplit: D3W8A8_KSPLIT_AUTO (chosen from the shape and the workspace size),
- *           or 1..32 (>1 needs a DMA tile and K / 64 >= ksplit).
+ *           or 1..32 (>1 needs a 128x128 DMA tile, 5 or 7, and at least
+ *           one K step per split).
  *   workspace: device memory, 256-byte aligned, `workspace_bytes` long, of
  *           any contents (it holds partial sums between the two launches).
  *           Calls that share a workspace must be ordered (same stream);

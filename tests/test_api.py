@@ -140,13 +140,12 @@ def test_split_k_plan_on_the_host():
     lib = _lib.load()
     big = 64 << 20
     slot = 128 * 128 * 4
-    # 128 rows x 4096 columns: 32 tiles of 128x128 leave the GPU idle -> 16 splits of 4 K steps each
-    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, big) == \
-        32 * 16 * slot
+    # 128 rows x 4096 columns: 32 tiles of 128x128 leave the GPU idle -> 4 splits of 1 KiB of K each
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, big) == 32 * 4 * slot
+    # down projection (K = 12288): 8 splits make ~one workgroup per CU
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 12288, 12288, 12288, -1, -1, big) == 32 * 8 * slot
     # a smaller workspace lowers the automatic split; none at all means no split
-    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1,
-                                     32 * 5 * slot) == \
-        32 * 5 * slot
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, 32 * 3 * slot) == 32 * 3 * slot
     assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, 0) == 0
     # state-pass shapes fill the GPU without splitting
     assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, -1, -1, big) == 0
@@ -158,7 +157,8 @@ def test_split_k_plan_on_the_host():
     assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, 5, 4, 1 << 20) == -1
     assert b"too small" in lib.d3w8a8_last_error()
     assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, 1, 2, big) == -1  # register-staged tile
-    assert b"pipelined" in lib.d3w8a8_last_error()
+    assert b"128x128" in lib.d3w8a8_last_error()
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, 4, 2, big) == -1  # 256x256 tile
     dummy = 256
     assert lib.d3w8a8_gemm_ws(0, dummy, 4096, dummy, dummy, 4096, dummy, 128, 4096, 4096, 0, 0, dummy, 4096,
                               None, 0, None, None, 5, 4, dummy, 1 << 20, None) == _lib.EINVAL

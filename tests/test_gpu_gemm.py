@@ -25,10 +25,12 @@ TILES = list(_lib.TILES)
 
 
 def _dma_needs_k64(tile, Kd, a, w) -> bool:
-    """The pipelined (DMA) tiles take K % 64 == 0 only; other K must be refused, not computed."""
-    if tile in _lib.DMA_TILES and Kd % 64:
+    """The pipelined (DMA) tiles take K % 64 == 0 (K % 128 for the 128-byte-step tile) only; other K must be
+    refused, not computed."""
+    mult = _lib.tile_k_multiple(tile)
+    if tile in _lib.DMA_TILES and Kd % mult:
         mode = "int8" if a.dtype == torch.int8 else "fp8"
-        with pytest.raises(ValueError, match="K % 64"):
+        with pytest.raises(ValueError, match=f"K % {mult}"):
             K.gemm(mode, a.to("cuda"), None, w.to("cuda"), None, epilogue=_lib.EPI_RAW, tile=tile)
         return True
     return False

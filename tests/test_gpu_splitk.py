@@ -25,31 +25,45 @@ SHAPES = [(128, 1024, 4096), (77, 200, 448), (16, 640, 2048), (130, 384, 1024), 
 SPLITS = [2, 3, 7, 16]
 
 
-def _splits(Kd):
-    return [s for s in SPLITS if s <= Kd // 64]
+def _splits(Kd, tile=_lib.TILE_DMA_128_W4):
+    return [s for s in SPLITS if s <= Kd // _lib.tile_k_multiple(tile)]
 
 
-@pytest.mark.parametrize("tile", _lib.DMA_TILES)
+SPLIT_TILES = (_lib.TILE_DMA_128_W4, _lib.TILE_DMA_128_W4_K128)
+
+
+def test_split_needs_a_128_tile(dev):
+    a = torch.zeros(128, 1024, dtype=torch.int8, device=dev)
+    for tile in set(_lib.TILES) - set(SPLIT_TILES):
+        with pytest.raises(ValueError, match="128x128"):
+            K.gemm("int8", a, None, a, None, epilogue=_lib.EPI_RAW, tile=tile, ksplit=2)
+
+
+@pytest.mark.parametrize("tile", SPLIT_TILES)
 @pytest.mark.parametrize("M,N,Kd", SHAPES)
 def test_int8_split_accumulators_exact(dev, tile, M, N, Kd):
+    if Kd % _lib.tile_k_multiple(tile):
+        pytest.skip("K is not a multiple of this tile's step (refusal covered in test_gpu_gemm)")
     g = gen(M * 7 + N + Kd)
     a, w = rand_i8(g, M, Kd), rand_i8(g, N, Kd)
     ref = R.int_accumulate(a, w)
     ad, wd = a.to(dev), w.to(dev)
-    for s in _splits(Kd) + [_lib.KSPLIT_AUTO]:
+    for s in _splits(Kd, tile) + [_lib.KSPLIT_AUTO]:
         acc = K.gemm("int8", ad, None, wd, None, epilogue=_lib.EPI_RAW, tile=tile, ksplit=s)
         assert torch.equal(acc.cpu().to(torch.int64), ref), f"ksplit {s}"
 
 
-@pytest.mark.parametrize("tile", [_lib.TILE_DMA_128_W4, _lib.TILE_DMA_256_W4])
+@pytest.mark.parametrize("tile", SPLIT_TILES)
 @pytest.mark.parametrize("M,N,Kd", SHAPES)
 def test_fp8_split_reproducible_and_bounded(dev, tile, M, N, Kd):
+    if Kd % _lib.tile_k_multiple(tile):
+        pytest.skip("K is not a multiple of this tile's step")
     g = gen(M * 5 + N * 3 + Kd)
     a, w = rand_fp8(g, M, Kd), rand_fp8(g, N, Kd)
     ref = R.fp8_accumulate(a, w)
     bound = (a.double().abs() @ w.double().abs().t()) * 2.0 ** -14 + 1e-30
     ad, wd = a.to(dev), w.to(dev)
-    for s in _splits(Kd):
+    for s in _splits(Kd, tile):
         acc = K.gemm("fp8", ad, None, wd, None, epilogue=_lib.EPI_RAW, tile=tile, ksplit=s)
         again = K.gemm("fp8", ad, None, wd, None, epilogue=_lib.EPI_RAW, tile=tile, ksplit=s)
         assert torch.equal(acc.view(torch.int32), again.view(torch.int32)), f"ksplit {s} not reproducible"
