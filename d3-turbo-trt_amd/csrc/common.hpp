@@ -86,37 +86,71 @@ __device__ __forceinline__ float round_to(float v) {
 
 // ---- quantization of one value ------------------------------------------------
 // The reference divides every element by its row's fp32 scale (x / scale,
-// quant.py:86, 100). With rd = RN64(1 / scale) formed once per row,
-//   RN32(RN64(x * rd)) == RN32(x / scale)
-// for every finite fp32 x and normal scale: the double product is within
-// 2^-51.9 (relative) of x / scale, while x / scale is either an fp32 value or
-// more than 2^-49 (relative) away from every fp32 rounding midpoint (its
-// distance is a multiple of 2^min(ex, em + es) over a product of at most 49
-// significant bits), and it is never a midpoint itself (x = midpoint * scale
-// would need 25 significant bits in x). Three VALU ops per element replace the
-// ~10 of a correctly rounded fp32 division.
+// quant.py:86, 100). With r = RN(1 / scale) formed once per row (a correctly
+// rounded fp32 division), Markstein's correction step
+//   q = RN(x * r);  e = RN(x - q * scale) (FMA, exact);  q' = RN(e * r + q) (FMA)
+// gives q' == RN(x / scale) bit for bit whenever |x| >= 2^-100 and the quotient
+// is a normal float: r is the correctly rounded reciprocal and q lies within
+// one ulp of x / scale. Below that the residual can underflow, but then both
+// q' and x / scale are below 2^-40 in magnitude and round to the same signed
+// zero in int8 and FP8 once the sign of x is put back on q'. Three VALU ops
+// per element replace a correctly rounded fp32 division (~10 ops); the
+// exhaustive CPU check of this identity is tests/c/fma_division.c.
 struct RowScale {
   float s;
-  double rd;
+  float r;
 };
-__device__ __forceinline__ RowScale make_row_scale(float s) { return RowScale{s, 1.0 / (double)s}; }
-__device__ __forceinline__ float div_row(float x, const RowScale& r) { return (float)((double)x * r.rd); }
+__device__ __forceinline__ RowScale make_row_scale(float s) { return RowScale{s, 1.0f / s}; }
+__device__ __forceinline__ float div_row(float x, const RowScale& r) {
+  const float q = x * r.r;
+  const float e = __builtin_fmaf(-q, r.s, x);
+  return __builtin_fmaf(e, r.r, q);
+}
 
-// int8: clamp(rint(x / scale), -127, 127) (quant.py:86, 100). Clamping before
-// rounding gives the same integers (127.5 rounds to 128, then clamps to 127;
-// clamped first it stays 127). Adding 1.5 * 2^23 rounds to nearest even and
-// leaves the integer, two's complement, in the low byte of the float's bits.
-__device__ __forceinline__ uint32_t quant_i8_bits(float x, const RowScale& r) {
-  float v = fminf(fmaxf(div_row(x, r), -kInt8Max), kInt8Max);
+// int8: clamp(rint(x / scale), -127, 127) (quant.py:86, 100). Adding 1.5 * 2^23
+// rounds to nearest even and leaves the integer, two's complement, in the low
+// byte of the float's bits (the sign of a zero quotient does not matter).
+// CLAMP: when the scale comes from the amax of the very values quantized
+// (scale = RN(amax / 127), |x| <= amax), |x / scale| <= 127 (1 + 2^-23), which
+// rounds to at most 127, so the reference's clamp never acts and is skipped;
+// a row amax supplied from outside keeps it. Clamping before rounding gives
+// the same integers as after (127.5 rounds to 128, then clamps to 127).
+template <bool CLAMP>
+__device__ __forceinline__ uint32_t quant_i8_word(float x, const RowScale& r) {  // int8 in the low byte
+  float v = div_row(x, r);
+  if constexpr (CLAMP) v = fminf(fmaxf(v, -kInt8Max), kInt8Max);
   v = v + 12582912.0f;
-  return __float_as_uint(v) & 0xffu;
+  return __float_as_uint(v);
+}
+template <bool CLAMP>
+__device__ __forceinline__ uint32_t quant_i8_bits(float x, const RowScale& r) {
+  return quant_i8_word<CLAMP>(x, r) & 0xffu;
 }
 // fp8: e4m3fn_rne(clamp(x / scale, -448, 448))   (quant.py:83, 98); the
-// hardware converter rounds to nearest even and is OCP E4M3 on gfx950.
+// hardware converter rounds to nearest even and is OCP E4M3 on gfx950. The
+// quotient carries the sign of x also when it is zero (-0 encodes as 0x80).
+__device__ __forceinline__ float div_row_signed(float x, const RowScale& r) {
+  const float q = div_row(x, r);
+  return __uint_as_float((__float_as_uint(q) & 0x7fffffffu) | (__float_as_uint(x) & 0x80000000u));
+}
 __device__ __forceinline__ uint32_t quant_f8_pair(float x0, float x1, const RowScale& r) {
-  float a = fminf(fmaxf(div_row(x0, r), -kFp8Max), kFp8Max);
-  float b = fminf(fmaxf(div_row(x1, r), -kFp8Max), kFp8Max);
+  float a = fminf(fmaxf(div_row_signed(x0, r), -kFp8Max), kFp8Max);
+  float b = fminf(fmaxf(div_row_signed(x1, r), -kFp8Max), kFp8Max);
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+}
+// four values -> four E4M3 bytes of one word (the second conversion writes the high half)
+__device__ __forceinline__ uint32_t quant_f8_quad(const float* x, const RowScale& r) {
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = fminf(fmaxf(div_row_signed(x[i], r), -kFp8Max), kFp8Max);
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], lo, true);
+}
+// four int8 results (the low bytes of quant_i8_bits words) -> one word, by byte permutes
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+  const uint32_t a = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);  // [b0.0, b1.0, 0, 0]
+  const uint32_t c = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);  // [b2.0, b3.0, 0, 0]
+  return __builtin_amdgcn_perm(c, a, 0x05040100u);                // [b0.0, b1.0, b2.0, b3.0]
 }
 
 // ---- wave reductions (64 lanes) --------------------------------------------------

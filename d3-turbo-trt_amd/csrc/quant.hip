@@ -149,19 +149,19 @@ __device__ __forceinline__ void store8(void* p, const float* v) {
   }
 }
 
-// Quantize 8 values with a row scale and store 8 bytes at q.
-template <int MODE>
+// Quantize 8 values with a row scale and store 8 bytes at q (CLAMP: see quant_i8_bits).
+template <int MODE, bool CLAMP = false>
 __device__ __forceinline__ void quant_store8(void* q, const float* v, const RowScale& r) {
   uint32_t lo, hi;
   if constexpr (MODE == kInt8) {
     uint32_t b[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) b[i] = quant_i8_bits(v[i], r);
-    lo = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-    hi = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    for (int i = 0; i < 8; ++i) b[i] = quant_i8_word<CLAMP>(v[i], r);
+    lo = pack_low_bytes(b[0], b[1], b[2], b[3]);
+    hi = pack_low_bytes(b[4], b[5], b[6], b[7]);
   } else {
-    lo = quant_f8_pair(v[0], v[1], r) | (quant_f8_pair(v[2], v[3], r) << 16);
-    hi = quant_f8_pair(v[4], v[5], r) | (quant_f8_pair(v[6], v[7], r) << 16);
+    lo = quant_f8_quad(v, r);
+    hi = quant_f8_quad(v + 4, r);
   }
   *(uint2*)q = make_uint2(lo, hi);
 }
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256) void quant_rows_generic(const void* __restrict
   uint8_t* qr = (uint8_t*)q + row * ldq;
   for (int64_t k = lane; k < K; k += 64) {
     const float xv = load_elem<DT>(x, base + k);
-    if constexpr (MODE == kInt8) qr[k] = (uint8_t)quant_i8_bits(xv, s);
+    if constexpr (MODE == kInt8) qr[k] = (uint8_t)quant_i8_bits<false>(xv, s);
     else qr[k] = (uint8_t)(quant_f8_pair(xv, 0.0f, s) & 0xff);
   }
   if (lane == 0) scale[row] = s.s;
@@ -246,7 +246,7 @@ __global__ __launch_bounds__(256) void quant_rows_amax_vec(const void* __restric
     if (RC::valid(c, lane, K)) {
       float v[8];
       h_.get(c, v);
-      quant_store8<MODE>(qr + RC::col(c, lane), v, s);
+      quant_store8<MODE, true>(qr + RC::col(c, lane), v, s);  // amax from outside: keep the clamp
     }
   }
   if (lane == 0) scale[row] = s.s;
@@ -264,15 +264,45 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
     const void* __restrict__ x, int64_t ldx, const void* __restrict__ w, int64_t M, int64_t K,
     float eps, void* __restrict__ q, int64_t ldq, float* __restrict__ scale,
     void* __restrict__ normed, int64_t ldn, float* __restrict__ clear_amax) {
+  extern __shared__ __attribute__((aligned(16))) float gain_lds[];  // K floats: g = 1 + w (ZC) or w
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
-  if (row >= M) return;
+  const bool live = row < M;
   using RC = RowChunks<DT, NCH>;
-  using RW = RowChunks<DTW, NCH>;
   RC x_;
-  x_.load((const char*)x + row * ldx * RC::kES, K, lane);
-  RW w_;
-  w_.load((const char*)w, K, lane);
+  if (live) x_.load((const char*)x + row * ldx * RC::kES, K, lane);
+  // The gain is the same for every row: the block forms it once in fp32 (the
+  // values the reference's (1 + w.float()) holds) and every wave reads it from
+  // LDS, instead of each wave loading and widening the weight row.
+  {
+    // 8-element pieces of w, all loads issued before any is used (K % 8 == 0, w 16-byte aligned)
+    using RW = RowChunks<DTW, 1>;
+    constexpr int PIECES = (NCH * 64 + 255) / 256;  // per thread: NCH * 64 pieces over 256 threads
+    RW wp[PIECES];
+#pragma unroll
+    for (int i = 0; i < PIECES; ++i) {
+      const int64_t k = (int64_t)(threadIdx.x + 256 * i) * 8;
+      if (k < K) {
+        const uint4* src = (const uint4*)((const char*)w + k * RW::kES);
+#pragma unroll
+        for (int u = 0; u < RW::kWords; ++u) wp[i].raw[0][u] = src[u];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PIECES; ++i) {
+      const int64_t k = (int64_t)(threadIdx.x + 256 * i) * 8;
+      if (k < K) {
+        float g[8];
+        wp[i].get(0, g);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) g[u] = ZC ? 1.0f + g[u] : g[u];
+        *(float4*)(gain_lds + k) = make_float4(g[0], g[1], g[2], g[3]);
+        *(float4*)(gain_lds + k + 4) = make_float4(g[4], g[5], g[6], g[7]);
+      }
+    }
+  }
+  __syncthreads();
+  if (!live) return;
   // sum of squares: for 16-bit inputs one v_dot2 per packed pair (the squares of bf16 / fp16 values
   // are exact in fp32, as torch's x.float().pow(2) is)
   float ss = 0.0f;
@@ -303,14 +333,16 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     if (RC::valid(c, lane, K)) {
-      float v[8], g[8];
+      float v[8];
       x_.get(c, v);
-      w_.get(c, g);
+      const float4 g0 = *(const float4*)(gain_lds + RC::col(c, lane));
+      const float4 g1 = *(const float4*)(gain_lds + RC::col(c, lane) + 4);
+      const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
 #pragma unroll
       for (int i = 0; i < 8; i += 2) {
         float p0 = v[i] * rstd, p1 = v[i + 1] * rstd;
-        p0 = p0 * (ZC ? 1.0f + g[i] : g[i]);
-        p1 = p1 * (ZC ? 1.0f + g[i + 1] : g[i + 1]);
+        p0 = p0 * g[i];
+        p1 = p1 * g[i + 1];
         round_pair_to<DT>(p0, p1);
         y[c][i] = p0;
         y[c][i + 1] = p1;
@@ -452,9 +484,10 @@ hipError_t launch_rmsnorm_quant_t(const void* x, int64_t ldx, const void* w, int
                                   int zc, void* q, int64_t ldq, float* scale, void* normed, int64_t ldn,
                                   float* clear_amax, hipStream_t st) {
   if (M == 0) return hipSuccess;
+  const size_t lds = (size_t)K * sizeof(float);  // the staged gain (K <= kMaxVecK: at most 64 KiB)
 #define L(N)                                                                                                        \
-  if (zc) hipLaunchKernelGGL((rmsnorm_quant_vec<MODE, DT, DTW, N, true>), quant_grid(M), dim3(256), 0, st, x, ldx, w, M, K, eps, q, ldq, scale, normed, ldn, clear_amax); \
-  else hipLaunchKernelGGL((rmsnorm_quant_vec<MODE, DT, DTW, N, false>), quant_grid(M), dim3(256), 0, st, x, ldx, w, M, K, eps, q, ldq, scale, normed, ldn, clear_amax)
+  if (zc) hipLaunchKernelGGL((rmsnorm_quant_vec<MODE, DT, DTW, N, true>), quant_grid(M), dim3(256), lds, st, x, ldx, w, M, K, eps, q, ldq, scale, normed, ldn, clear_amax); \
+  else hipLaunchKernelGGL((rmsnorm_quant_vec<MODE, DT, DTW, N, false>), quant_grid(M), dim3(256), lds, st, x, ldx, w, M, K, eps, q, ldq, scale, normed, ldn, clear_amax)
   D3_NCH_DISPATCH(K, L);
 #undef L
   return hipGetLastError();

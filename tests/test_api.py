@@ -164,3 +164,4 @@ def test_split_k_plan_on_the_host():
                               None, 0, None, None, 5, 4, dummy, 1 << 20, None) == _lib.EINVAL
     header = open(os.path.join(ROOT, "include", "d3w8a8.h")).read()
     assert re.search(r"#define D3W8A8_KSPLIT_AUTO \((-?\d+)\)", header).group(1) == str(_lib.KSPLIT_AUTO)
+
