@@ -15,6 +15,8 @@ the path, each timed on the GPU with HIP events on the launch stream:
                        launch per projection (K = 4096; N = 6144, 4096, 24576)
   mlp_block_int8       norm + quant -> gate_up + SwiGLU -> requant -> down + residual,
                        M = 4096, hidden 4096, intermediate 12288
+  question_gemms_fp8_m128  the four projections at M = 128 (a batch of 8 question blocks),
+                       weights streamed from HBM (pool > Infinity Cache): HBM GB/s
   linear_stack_fp8     48 layers of QKV / o_proj / MLP block, identity mixer: one
                        8192-token state pass, then 255 question blocks of 16 tokens
                        (ragged batches of 8 blocks, and of all 255)
@@ -372,6 +374,52 @@ def run_linear_stack(args):
     return res
 
 
+def run_question_gemms(args):
+    """The four projections at question-batch M = 128 (8 blocks x 16 tokens), FP8: HBM-bound weight
+    streams. Each call reads a different weight copy from a pool of > 600 MB, so no call finds its
+    weights in the 256 MB Infinity Cache; weight GB/s and algorithmic GB/s against 8 TB/s."""
+    import torch
+
+    from d3trt_amd import _lib
+    from d3trt_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    M, out = 128, {}
+    gen = torch.Generator(device=dev).manual_seed(0)
+    lib = _lib.load()
+    for name, (N, Kd) in (("qkv", (6144, 4096)), ("o_proj", (4096, 4096)), ("gate_up", (24576, 4096)),
+                          ("down", (4096, 12288))):
+        copies = max(2, -(-(600 << 20) // (N * Kd)))
+        ws = [(torch.randn(N, Kd, generator=gen, device=dev) * 8).to(torch.float8_e4m3fn) for _ in range(copies)]
+        w_s = torch.rand(N, generator=gen, device=dev) * 1e-3
+        a = (torch.randn(M, Kd, generator=gen, device=dev) * 8).to(torch.float8_e4m3fn)
+        a_s = torch.rand(M, generator=gen, device=dev) * 1e-3
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        calls = 4 * copies
+        for i in range(copies):
+            K.gemm("fp8", a, a_s, ws[i], w_s, out=y)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(calls):
+            K.gemm("fp8", a, a_s, ws[i % copies], w_s, out=y)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / calls * 1e3
+        ws_bytes = lib.d3w8a8_gemm_workspace(M, N, Kd, Kd, Kd, -1, -1, K.WORKSPACE_BYTES)
+        tiles = ((M + 127) // 128) * ((N + 127) // 128)
+        out[name] = {"M": M, "N": N, "K": Kd, "us": round(us, 2),
+                     "weight_gbs": round(N * Kd / (us * 1e-6) / 1e9, 1),
+                     "algo_gbs": round(gemm_bytes(M, N, Kd) / (us * 1e-6) / 1e9, 1),
+                     "frac_hbm": round(gemm_bytes(M, N, Kd) / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 3),
+                     "ksplit": ws_bytes // (tiles * 128 * 128 * 4) if ws_bytes > 0 else 1}
+        del ws
+        torch.cuda.empty_cache()
+    out["note"] = ("per-call HIP-event time, weights rotated over > 600 MB; tile 7 (128-byte K steps) with "
+                   "automatic split-K; includes the split-K reduce launch")
+    return out
+
+
 # ---------------------------------------------------------------------------------------------
 # CPU baseline: the oracle's restatement of the reference CPU path
 # ---------------------------------------------------------------------------------------------
@@ -466,7 +514,8 @@ def main() -> int:
     if not args.headline_only:
         configs = {}
         for name, fn in (("single_int8_linear", run_single_linear), ("ragged_int8", run_ragged),
-                         ("mlp_block_int8", run_mlp_block), ("linear_stack_fp8", run_linear_stack)):
+                         ("mlp_block_int8", run_mlp_block), ("question_gemms_fp8_m128", run_question_gemms),
+                         ("linear_stack_fp8", run_linear_stack)):
             configs[name] = fn(args)
             print(json.dumps({"progress": name, "done": True}), file=sys.stderr, flush=True)
         result["configs"] = configs
