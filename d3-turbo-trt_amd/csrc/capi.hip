@@ -136,7 +136,7 @@ static int gemm_impl(int mode, const void* a, int64_t lda, const float* a_scale,
   if (epilogue < D3W8A8_EPI_DEQUANT || epilogue > D3W8A8_EPI_RESIDUAL)
     return fail(D3W8A8_EINVAL, "gemm: unknown epilogue %d", epilogue);
   if (epilogue != D3W8A8_EPI_RAW && !dtype_ok(out_dtype)) return fail(D3W8A8_EINVAL, "gemm: unknown out dtype");
-  if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_128_W4_K128) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
+  if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_256x192_W4) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
   if (ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) return fail(D3W8A8_EINVAL, "gemm: bad ksplit %d", ksplit);
   if (workspace_bytes < 0 || (workspace_bytes > 0 && (!workspace || !aligned(workspace, 256))))
     return fail(D3W8A8_EINVAL, "gemm: the workspace must be 256-byte aligned device memory");
@@ -147,7 +147,7 @@ static int gemm_impl(int mode, const void* a, int64_t lda, const float* a_scale,
   const int64_t ncols = epilogue == D3W8A8_EPI_SWIGLU ? N / 2 : N;
   if (lda < K || ldw < K || lda % 16 || ldw % 16 || ldo < ncols)
     return fail(D3W8A8_EINVAL, "gemm: leading dimensions must cover the rows and be multiples of 16");
-  const d3::GemmPlan plan = d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, workspace_bytes);
+  const d3::GemmPlan plan = d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, workspace_bytes, epilogue);
   if (plan.error) return fail(D3W8A8_EINVAL, "gemm: %s", plan.error);
   if (M == 0 || N == 0) return D3W8A8_OK;
   if (!a || !w || !out || (epilogue != D3W8A8_EPI_RAW && (!a_scale || !w_scale)))
@@ -191,11 +191,13 @@ int d3w8a8_gemm_ws(int mode, const void* a, int64_t lda, const float* a_scale, c
 int64_t d3w8a8_gemm_workspace(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
                               int64_t max_bytes) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 16 || lda < K || ldw < K || M > INT32_MAX / 2 || N > INT32_MAX / 2 ||
-      tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_128_W4_K128 || ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) {
+      tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_256x192_W4 || ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) {
     fail(D3W8A8_EINVAL, "gemm_workspace: bad arguments");
     return -1;
   }
-  const d3::GemmPlan plan = d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, max_bytes < 0 ? 0 : max_bytes);
+  // the epilogue only rules tiles out; none of those it could rule out splits K, so the bytes do not depend on it
+  const d3::GemmPlan plan =
+      d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, max_bytes < 0 ? 0 : max_bytes, D3W8A8_EPI_DEQUANT);
   if (plan.error) {
     fail(D3W8A8_EINVAL, "gemm_workspace: %s", plan.error);
     return -1;

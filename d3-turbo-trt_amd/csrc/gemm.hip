@@ -64,6 +64,7 @@ TileShape shape_of(int tile) {
     case kDma128w4: return {128, 128, true, 64};
     case kDma256x128w4: return {256, 128, true, 64};
     case kDma128w4k128: return {128, 128, true, 128};
+    case kDma256x192w4: return {256, 192, true, 64};
   }
   return {0, 0, false, 0};
 }
@@ -77,18 +78,31 @@ bool dma_offsets_fit(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) 
   return (M - 1) * lda + K < lim && (N - 1) * ldw + K < lim;
 }
 
+// Rounds of tiles the chip runs one after the other (one workgroup per CU).
+int64_t rounds(int64_t tiles) { return (tiles + kCUs - 1) / kCUs; }
+
 // Tile choice (measured on MI355X): with K % 64 == 0, the 4-wave 256x256 DMA
 // tile once there are enough such tiles to cover the chip, 256x128 for
-// mid-size problems, 128x128 otherwise. M <= 128 (a 256-row tile would compute
-// half its rows for nothing) streams the weights: 128x128 with 128-byte K
-// steps when K allows.
-int choose_tile(int64_t M, int64_t N, int64_t K, bool fit) {
+// mid-size problems, 128x128 otherwise. Where 256x256 tiles leave the last
+// round partly idle (fused QKV at M = 4096, N = 6144: 384 tiles, 1.5 rounds)
+// and 256x192 tiles fill whole rounds (512 tiles, 2 rounds), the narrower
+// tile wins: it is taken when its rounds x tile area is at least 10% below
+// that of 256x256 (N % 192 == 0, epilogues without gate/up pairs). M <= 128 (a
+// 256-row tile would compute half its rows for nothing) streams the weights:
+// 128x128 with 128-byte K steps when K allows.
+int choose_tile(int64_t M, int64_t N, int64_t K, bool fit, int epi) {
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
   if (K % 64 == 0 && fit) {
     if (M <= 128) return K % 128 == 0 ? kDma128w4k128 : kDma128w4;
-    if (t256 >= 192) return kDma256w4;
+    if (t256 >= 192) {
+      if (epi != kEpiSwiGLU && N % 192 == 0) {
+        const int64_t t192 = ((M + 255) / 256) * (N / 192);
+        if (rounds(t192) * 192 * 10 <= rounds(t256) * 256 * 9) return kDma256x192w4;
+      }
+      return kDma256w4;
+    }
     if (t256x128 >= 160) return kDma256x128w4;
     return kDma128w4;
   }
@@ -113,12 +127,14 @@ int choose_ksplit(int64_t tiles, int nk, int bk) {
 }  // namespace
 
 GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
-                   int64_t ws_bytes) {
+                   int64_t ws_bytes, int epi) {
   GemmPlan pl{};
   pl.ksplit = 1;
   const bool fit = dma_offsets_fit(M, N, K, lda, ldw);
-  pl.tile = tile < 0 ? choose_tile(M, N, K, fit) : tile;
+  pl.tile = tile < 0 ? choose_tile(M, N, K, fit, epi) : tile;
   if (pl.tile >= kTileCount) return pl.error = "unknown tile", pl;
+  if (pl.tile == kDma256x192w4 && epi == kEpiSwiGLU)
+    return pl.error = "the 256x192 tile has 3 column blocks per wave; SwiGLU needs gate/up pairs", pl;
   const TileShape sh = shape_of(pl.tile);
   if (sh.dma && K % sh.bk != 0)
     return pl.error = sh.bk == 128 ? "the 128-byte-step tile needs K % 128 == 0" : "the pipelined tiles need K % 64 == 0",

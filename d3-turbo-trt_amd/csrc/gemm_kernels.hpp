@@ -872,6 +872,9 @@ hipError_t launch_epi(GemmParams p, int tile, hipStream_t st) {
     case kDma128w4: return launch_dma<MODE, 128, 128, 2, 2, EPI, OUT>(p, st);
     case kDma256x128w4: return launch_dma<MODE, 256, 128, 2, 2, EPI, OUT>(p, st);
     case kDma128w4k128: return launch_dma<MODE, 128, 128, 2, 2, EPI, OUT, 128>(p, st);
+    case kDma256x192w4:
+      if constexpr (EPI == kEpiSwiGLU) return hipErrorInvalidValue;  // 3 column blocks per wave: no gate/up pairs
+      else return launch_dma<MODE, 256, 192, 2, 2, EPI, OUT>(p, st);
   }
   return hipErrorInvalidValue;
 }

@@ -57,7 +57,8 @@ enum TileCfg : int {
   kDma128w4 = 5,     // DMA pipeline 128x128, 4 waves (64x64 each), 4 stages
   kDma256x128w4 = 6, // DMA pipeline 256x128, 4 waves (128x64 each), 4 stages
   kDma128w4k128 = 7, // DMA pipeline 128x128, 4 waves, 128-byte K steps (weight streaming, K % 128 == 0)
-  kTileCount = 8
+  kDma256x192w4 = 8, // DMA pipeline 256x192, 4 waves (128x96 each), 4 stages; not for SwiGLU
+  kTileCount = 9
 };
 
 constexpr int kMaxKSplit = 32;
@@ -70,8 +71,9 @@ struct GemmPlan {
   int64_t ws_bytes;  // workspace the plan uses (0 when ksplit == 1)
   const char* error; // non-null: the request is not valid
 };
+// `epi` (an Epilogue) rules out tiles the epilogue cannot use.
 GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
-                   int64_t ws_bytes);
+                   int64_t ws_bytes, int epi);
 // Launches the plan; p.partial must point to a workspace of plan.ws_bytes.
 hipError_t launch_gemm(int mode, GemmParams p, int epi, int out_dt, const GemmPlan& plan, hipStream_t st);
 

@@ -1,0 +1,164 @@
+// Fused zero-centred RMSNorm + per-token quantization for gfx950.
+//
+//   y = DT( (x * rstd) * g ),  g = 1 + w (zero_centered) or w,
+//   rstd = 1 / sqrt(sum(x*x) / K + eps)  (sqrt and division each correctly rounded), then q(y).
+//
+// RMSNorm is transformers' Qwen3_5RMSNorm (modeling_qwen3_5.py:720-734), the
+// norm TRT-LLM's RMSNorm(use_gemma=True) applies before each linear group
+// (d3trt/model/trtllm_stack.py:217-228, core.py:207, 215); the quantization
+// is d3trt/model/quant.py:92-100.
+//
+// Optional outputs: the normed rows y, and clear_amax[row] = 0 (the SwiGLU
+// row-amax buffer of the same rows, so the next GEMM can atomically max into
+// it without a memset).
+#include "quant_common.hpp"
+
+namespace d3 {
+
+template <int MODE, int DT, int DTW, int NCH, bool FULL>
+__global__ __launch_bounds__(256) void rmsnorm_quant_vec(
+    const void* __restrict__ x, int64_t ldx, const void* __restrict__ w, int64_t M, int64_t K,
+    float eps, int zc, void* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+    void* __restrict__ normed, int64_t ldn, float* __restrict__ clear_amax) {
+  extern __shared__ __attribute__((aligned(16))) float gain_lds[];  // K floats: g = 1 + w (zc) or w
+  const int lane = threadIdx.x & 63;
+  const int64_t row0 = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+  using RC = RowChunks<DT, NCH, FULL>;
+  // Waves past the last row still take part in the gain set-up and its barrier.
+  const bool live = row0 < M;
+  auto stage_gain = [&] {
+    // The gain is the same for every row: the block forms it once in fp32 (the
+    // values the reference's (1 + w.float()) holds) and every wave reads it from
+    // LDS, instead of each wave loading and widening the weight row.
+    {
+      using RW = RowChunks<DTW, 1, true>;
+      constexpr int PIECES = (NCH * 64 + 255) / 256;  // 8-element pieces per thread: NCH * 64 over 256 threads
+      RW wp[PIECES];
+#pragma unroll
+      for (int i = 0; i < PIECES; ++i) {
+        const int64_t k = (int64_t)(threadIdx.x + 256 * i) * 8;
+        if (k < K) {
+          const uint4* src = (const uint4*)((const char*)w + k * RW::kES);
+#pragma unroll
+          for (int u = 0; u < RW::kWords / 4; ++u) {
+            const uint4 t = src[u];
+            wp[i].w[0][4 * u] = t.x;
+            wp[i].w[0][4 * u + 1] = t.y;
+            wp[i].w[0][4 * u + 2] = t.z;
+            wp[i].w[0][4 * u + 3] = t.w;
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < PIECES; ++i) {
+        const int64_t k = (int64_t)(threadIdx.x + 256 * i) * 8;
+        if (k < K) {
+          float g[8];
+          wp[i].get(0, g);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) g[u] = zc ? 1.0f + g[u] : g[u];
+          *(float4*)(gain_lds + k) = make_float4(g[0], g[1], g[2], g[3]);
+          *(float4*)(gain_lds + k + 4) = make_float4(g[4], g[5], g[6], g[7]);
+        }
+      }
+    }
+    __syncthreads();
+  };
+  if (!live) {
+    stage_gain();
+    return;
+  }
+  pipeline_rows<RC>(
+      (const char*)x, ldx * RC::kES, row0, (int64_t)gridDim.x * kQuantWaves, M, K, lane, stage_gain, [&](RC& x_, int64_t row) {
+        // sum of squares: for 16-bit inputs one v_dot2 per packed pair (the squares of bf16 / fp16
+        // values are exact in fp32, as torch's x.float().pow(2) is)
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          if (RC::valid(c, lane, K)) {
+            if constexpr (DT == kF32) {
+              float v[8];
+              x_.get(c, v);
+#pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                const float sq = v[i] * v[i];
+                ss = ss + sq;
+              }
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) ss = dot2_sq<DT>(x_.w[c][i], ss);
+            }
+          }
+        }
+        ss = wave_sum(ss);
+        const float var = ss / (float)K;
+        const float t = var + eps;
+        const float rstd = 1.0f / sqrtf(t);  // torch.rsqrt on the CPU: 1 / sqrt(t), each step correctly rounded
+        // y, rounded to DT, kept packed (the normed output is stored from these words as they are)
+        RC y;
+        float amax = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          if (RC::valid(c, lane, K)) {
+            float v[8];
+            x_.get(c, v);
+            const float4 g0 = *(const float4*)(gain_lds + RC::col(c, lane));
+            const float4 g1 = *(const float4*)(gain_lds + RC::col(c, lane) + 4);
+            const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+              float p0 = v[i] * rstd, p1 = v[i + 1] * rstd;
+              p0 = p0 * g[i];
+              p1 = p1 * g[i + 1];
+              y.put_pair(c, i / 2, p0, p1);
+              amax = fmaxf(fmaxf(amax, fabsf(p0)), fabsf(p1));
+            }
+          }
+        }
+        const RowScale s = scale_from_amax<MODE>(wave_max(amax));
+        if constexpr (NCH > 12) y.fence();  // wide rows: keep y packed between the passes (registers)
+        char* qr = (char*)q + row * ldq;
+        char* nr = normed ? (char*)normed + row * ldn * RC::kES : nullptr;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          if (RC::valid(c, lane, K)) {
+            const int64_t col = RC::col(c, lane);
+            float v[8];
+            y.get(c, v);
+            quant_store8<MODE>(qr + col, v, s);
+            if (nr) y.store_raw(c, nr + col * RC::kES);
+          }
+        }
+        if (lane == 0) {
+          scale[row] = s.s;
+          if (clear_amax) clear_amax[row] = 0.0f;
+        }
+      });
+}
+
+template <int MODE, int DT, int DTW>
+hipError_t launch_rmsnorm_quant_t(const void* x, int64_t ldx, const void* w, int64_t M, int64_t K, float eps,
+                                  int zc, void* q, int64_t ldq, float* scale, void* normed, int64_t ldn,
+                                  float* clear_amax, hipStream_t st) {
+  if (M == 0) return hipSuccess;
+  const size_t lds = (size_t)K * sizeof(float);  // the staged gain (K <= kMaxVecK: at most 64 KiB)
+#define L(N, F)                                                                                               \
+  hipLaunchKernelGGL((rmsnorm_quant_vec<MODE, DT, DTW, N, F>), row_grid(rmsnorm_quant_vec<MODE, DT, DTW, N, F>, M, lds), \
+                     dim3(256), lds, st, x, ldx, w, M, K, eps, zc, q, ldq, scale, normed, ldn, clear_amax)
+  D3_NCH_DISPATCH(K, L);
+#undef L
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_quant(int mode, int dt, int dtw, const void* x, int64_t ldx, const void* w, int64_t M,
+                                int64_t K, float eps, int zc, void* q, int64_t ldq, float* scale, void* normed,
+                                int64_t ldn, float* clear_amax, hipStream_t st) {
+  if (K > kMaxVecK) return hipErrorInvalidValue;
+#define C(MO, D, W) if (mode == MO && dt == D && dtw == W) return launch_rmsnorm_quant_t<MO, D, W>(x, ldx, w, M, K, eps, zc, q, ldq, scale, normed, ldn, clear_amax, st)
+  C(kInt8, kBF16, kBF16); C(kInt8, kBF16, kF32); C(kInt8, kF16, kF16); C(kInt8, kF16, kF32); C(kInt8, kF32, kF32);
+  C(kFp8, kBF16, kBF16); C(kFp8, kBF16, kF32); C(kFp8, kF16, kF16); C(kFp8, kF16, kF32); C(kFp8, kF32, kF32);
+#undef C
+  return hipErrorInvalidValue;
+}
+
+}  // namespace d3

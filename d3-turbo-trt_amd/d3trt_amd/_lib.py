@@ -23,9 +23,11 @@ MAX_SEGMENTS = 256  # D3W8A8_MAX_SEGMENTS: blocks of one ragged batch
 KSPLIT_AUTO = -1  # D3W8A8_KSPLIT_AUTO
 TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4 = 3, 4, 5, 6
 TILE_DMA_128_W4_K128 = 7  # 128-byte K steps: K % 128 == 0
+TILE_DMA_256x192_W4 = 8  # 3 column blocks per wave: not for the SwiGLU epilogue
 TILES = (TILE_256, TILE_128, TILE_64x128, TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4,
-         TILE_DMA_128_W4_K128)
-DMA_TILES = (TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4, TILE_DMA_128_W4_K128)
+         TILE_DMA_128_W4_K128, TILE_DMA_256x192_W4)
+DMA_TILES = (TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4, TILE_DMA_128_W4_K128,
+             TILE_DMA_256x192_W4)
 
 
 def tile_k_multiple(tile: int) -> int:
