@@ -4,9 +4,20 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <stdlib.h>
+#include <string.h>
+
 #include <algorithm>
 
 namespace d3 {
+
+bool gemm_persistent() {
+  static const bool on = [] {
+    const char* e = getenv("D3W8A8_GEMM_PERSIST");
+    return !(e && strcmp(e, "0") == 0);
+  }();
+  return on;
+}
 
 template <int MODE, int EPI, int OUT>
 hipError_t launch_epi(GemmParams p, int tile, hipStream_t st);

@@ -171,16 +171,25 @@ __device__ __forceinline__ void epilogue_edge(const GemmParams& p, ACC (&acc)[TM
 // them with 16-byte global stores, so every store instruction writes whole
 // cache lines. The residual (core.py:215: bf16 add of the rounded projection)
 // is applied in the read-back, where its loads are coalesced the same way.
-template <int TN, int EPI, int OUT>
+//
+// PACK: rows unpadded (RS = RB), the 16-byte chunk c of row r stored at chunk
+// c ^ (r & (CPR - 1)) (CPR a power of two, at most 16 used): 32 rows in 32 RB
+// bytes, for kernels whose LDS has no room for the padding; the lanes of one
+// write (32 rows, one chunk each) then meet each bank at most twice.
+template <int TN, int EPI, int OUT, bool PACK = false>
 struct EpiLds {
   static constexpr int ES = EPI == kEpiRaw ? 4 : (OUT == kF32 ? 4 : 2);  // output element bytes
   static constexpr int OC = EPI == kEpiSwiGLU ? TN * 16 : TN * 32;        // output columns per wave tile
   static constexpr int RB = OC * ES;                                      // bytes per output row
-  static constexpr int RS = RB + 16;                                      // padded LDS row stride
+  static constexpr int RS = PACK ? RB : RB + 16;                          // LDS row stride
   static constexpr int CPR = RB / 16;                                     // 16-byte chunks per row
   static constexpr int NRB = 32 * CPR / 64;                               // read-back chunks per lane
   static constexpr int BYTES = 32 * RS;                                   // LDS bytes per wave
+  static constexpr int SWZ = PACK ? (CPR < 16 ? CPR - 1 : 15) : 0;
   static_assert((32 * CPR) % 64 == 0, "read-back split");
+  static_assert(!PACK || (CPR & (CPR - 1)) == 0, "the packed layout needs a power-of-two chunk count");
+  // byte offset of byte `b` of row `row` in the staging area
+  __device__ static __forceinline__ int at(int row, int b) { return row * RS + ((((b >> 4) ^ (row & SWZ))) << 4) + (b & 15); }
 };
 
 template <int OUT, int ES>
@@ -195,10 +204,10 @@ __device__ __forceinline__ void lds_put4(uint8_t* dst, const float* v) {
   }
 }
 
-template <int MODE, int TM, int TN, int EPI, int OUT, bool MAP, typename ACC>
+template <int MODE, int TM, int TN, int EPI, int OUT, bool MAP, bool PACK, typename ACC, typename H>
 __device__ __forceinline__ void epilogue_lds(const GemmParams& p, ACC (&acc)[TM][TN], int64_t wrow0, int64_t wcol0,
-                                             int lane, uint8_t* stage) {
-  using E = EpiLds<TN, EPI, OUT>;
+                                             int lane, uint8_t* stage, H&& after_scales) {
+  using E = EpiLds<TN, EPI, OUT, PACK>;
   const int lrow = lane & 31, lhalf = lane >> 5;
   float st[TM];
   int64_t orow[TM];
@@ -222,7 +231,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmParams& p, ACC (&acc)[TM]
       }
   }
   const int64_t ocol0 = EPI == kEpiSwiGLU ? wcol0 / 2 : wcol0;  // first output column of the wave tile
-  uint8_t* my_row = stage + lrow * E::RS;
+  after_scales();
 
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -248,7 +257,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmParams& p, ACC (&acc)[TM]
             h[c] = round_to<OUT>(sl * uv);
             rmax = fmaxf(rmax, fabsf(h[c]));
           }
-          lds_put4<OUT, E::ES>(my_row + (jp * 32 + g * 8 + lhalf * 4) * E::ES, h);
+          lds_put4<OUT, E::ES>(stage + E::at(lrow, (jp * 32 + g * 8 + lhalf * 4) * E::ES), h);
           if (g == 3) __builtin_amdgcn_sched_barrier(0);
         }
       if (p.row_amax) {
@@ -260,7 +269,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmParams& p, ACC (&acc)[TM]
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          uint8_t* dst = my_row + (j * 32 + g * 8 + lhalf * 4) * E::ES;
+          uint8_t* dst = stage + E::at(lrow, (j * 32 + g * 8 + lhalf * 4) * E::ES);
           if constexpr (EPI == kEpiRaw) {
             if constexpr (MODE == kInt8)
               *(int4*)dst = make_int4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
@@ -285,7 +294,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmParams& p, ACC (&acc)[TM]
 #pragma unroll
     for (int t = 0; t < E::NRB; ++t) {
       const int q = t * 64 + lane, r = q / E::CPR, ch = q % E::CPR;
-      chunk[t] = *(const uint4*)(stage + r * E::RS + ch * 16);
+      chunk[t] = *(const uint4*)(stage + E::at(r, ch * 16));
       const int64_t orr = MAP ? __shfl(orow[i], r, 64) : wrow0 + i * 32 + r;
       obase[t] = orr;
     }
@@ -332,18 +341,28 @@ __device__ __forceinline__ void epilogue_lds(const GemmParams& p, ACC (&acc)[TM]
 
 // Full tiles (inside the output, vector-aligned) take the LDS path; edge tiles
 // check and store every element. `stage` is this wave's LDS region
-// (EpiLds::BYTES), free of any in-flight use when the epilogue starts.
-template <int MODE, int TM, int TN, int EPI, int OUT, typename ACC>
+// (EpiLds<.., PACK>::BYTES), free of any in-flight use when the epilogue
+// starts. after_scales() runs once the full path's row / channel scales are
+// in registers (the edge path runs it first): the persistent kernel issues
+// the next tile's DMA there, so the epilogue's own loads need not wait for it.
+template <int MODE, int TM, int TN, int EPI, int OUT, bool PACK = false, typename ACC, typename H>
 __device__ __forceinline__ void epilogue(const GemmParams& p, ACC (&acc)[TM][TN], int64_t wrow0, int64_t wcol0,
-                                         int lane, uint8_t* stage) {
+                                         int lane, uint8_t* stage, H&& after_scales) {
   const bool full = p.vec && wrow0 + TM * 32 <= p.M && wcol0 + TN * 32 <= p.N;
   if (full) {
-    if (EPI != kEpiSwiGLU && p.row_map) epilogue_lds<MODE, TM, TN, EPI, OUT, true>(p, acc, wrow0, wcol0, lane, stage);
-    else epilogue_lds<MODE, TM, TN, EPI, OUT, false>(p, acc, wrow0, wcol0, lane, stage);
+    if (EPI != kEpiSwiGLU && p.row_map)
+      epilogue_lds<MODE, TM, TN, EPI, OUT, true, PACK>(p, acc, wrow0, wcol0, lane, stage, after_scales);
+    else epilogue_lds<MODE, TM, TN, EPI, OUT, false, PACK>(p, acc, wrow0, wcol0, lane, stage, after_scales);
   } else {
+    after_scales();
     if (EPI != kEpiSwiGLU && p.row_map) epilogue_edge<MODE, TM, TN, EPI, OUT, true>(p, acc, wrow0, wcol0, lane);
     else epilogue_edge<MODE, TM, TN, EPI, OUT, false>(p, acc, wrow0, wcol0, lane);
   }
+}
+template <int MODE, int TM, int TN, int EPI, int OUT, typename ACC>
+__device__ __forceinline__ void epilogue(const GemmParams& p, ACC (&acc)[TM][TN], int64_t wrow0, int64_t wcol0,
+                                         int lane, uint8_t* stage) {
+  epilogue<MODE, TM, TN, EPI, OUT, false>(p, acc, wrow0, wcol0, lane, stage, [] {});
 }
 
 template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
@@ -626,6 +645,26 @@ __global__ __launch_bounds__(64) void gemm_splitk_reduce(GemmParams p) {
   epilogue<MODE, 1, TN, EPI, OUT>(p, acc, (int64_t)tm * BM + wm * WTM + i * 32, (int64_t)tn * BN + wn * WTN, lane, lds);
 }
 
+// Persistent form of the pipelined kernel: one workgroup per CU walks the
+// tiles blockIdx.x, + gridDim.x, ... and issues the next tile's DMA prologue
+// inside the current tile's epilogue, whose rows are then staged in an LDS
+// region of their own beside the stages (padded rows when they fit, else the
+// packed layout). Only where that region fits into the 160 KiB of LDS, for
+// 16-bit outputs of the dequantizing epilogues, and never with split-K.
+constexpr int kLdsBytes = 160 * 1024;
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT, int BK>
+struct PersistLayout {
+  static constexpr int NW = WM * WN, TN = BN / WN / 32;
+  static constexpr int STAGES = kStages * (BM + BN) * BK;
+  using Pad = EpiLds<TN, EPI, OUT, false>;
+  static constexpr bool kPadFits = STAGES + NW * Pad::BYTES <= kLdsBytes;
+  static constexpr bool kPackable = (Pad::CPR & (Pad::CPR - 1)) == 0;
+  static constexpr bool PACK = !kPadFits && kPackable;
+  using E = EpiLds<TN, EPI, OUT, PACK>;
+  static constexpr bool value =
+      !kSplitTile<BM, BN> && EPI != kEpiRaw && OUT != kF32 && STAGES + NW * E::BYTES <= kLdsBytes;
+};
+
 template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT, int BK>
 __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   using MF = Mfma<MODE>;
@@ -647,7 +686,9 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "DMA split");
   static_assert(EPI != kEpiSwiGLU || (TN % 2 == 0), "swiglu needs gate/up block pairs");
   static_assert(SLOTS >= 1, "tile too small for the interleave");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE];
+  using PL = PersistLayout<MODE, BM, BN, WM, WN, EPI, OUT, BK>;
+  constexpr bool PERSIST = PL::value;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE + (PERSIST ? NW * PL::E::BYTES : 0)];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -657,10 +698,10 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   // add it without spilling).
   const int S = kSplitTile<BM, BN> ? p.ksplit : 1;
   const int split = kSplitTile<BM, BN> ? (int)blockIdx.x % S : 0;
+  const int ntiles = p.tiles_m * p.tiles_n;
+  int tile = kSplitTile<BM, BN> ? (int)blockIdx.x / S : (int)blockIdx.x;
   int tm, tn;
-  if constexpr (kSplitTile<BM, BN>) tile_of((int)blockIdx.x / S, (int)gridDim.x / S, p.tiles_m, p.tiles_n, tm, tn);
-  else tile_of(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  int64_t m0, n0;
   const int nk_all = (int)(p.K / BK);
   const int kbeg = kSplitTile<BM, BN> ? (int)((int64_t)split * nk_all / S) : 0;
   // >= 1: the host keeps S <= nk_all
@@ -669,21 +710,30 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
 
   // DMA sources: uniform tile bases + per-lane 32-bit offsets (the host keeps every operand
   // offset below 2^32 for this kernel)
-  const uint8_t* a_base = uniform_ptr(p.a + m0 * p.lda + (int64_t)kbeg * BK);
-  const uint8_t* b_base = uniform_ptr(p.w + n0 * p.ldw + (int64_t)kbeg * BK);
+  const uint8_t* a_base;
+  const uint8_t* b_base;
   uint32_t a_off[A_DMA], b_off[B_DMA];
+  auto setup = [&](int t) {
+    if constexpr (kSplitTile<BM, BN>) tile_of(t, (int)gridDim.x / S, p.tiles_m, p.tiles_n, tm, tn);
+    else tile_of(t, ntiles, p.tiles_m, p.tiles_n, tm, tn);
+    m0 = (int64_t)tm * BM;
+    n0 = (int64_t)tn * BN;
+    a_base = uniform_ptr(p.a + m0 * p.lda + (int64_t)kbeg * BK);
+    b_base = uniform_ptr(p.w + n0 * p.ldw + (int64_t)kbeg * BK);
 #pragma unroll
-  for (int i = 0; i < A_DMA; ++i) {
-    const int row = (i * NW + wave) * RPD + lane / CPR;
-    const int ch = (lane % CPR) ^ lds_swz<BK>(row);
-    a_off[i] = (uint32_t)((min(m0 + row, p.M - 1) - m0) * p.lda + ch * 16);
-  }
+    for (int i = 0; i < A_DMA; ++i) {
+      const int row = (i * NW + wave) * RPD + lane / CPR;
+      const int ch = (lane % CPR) ^ lds_swz<BK>(row);
+      a_off[i] = (uint32_t)((min(m0 + row, p.M - 1) - m0) * p.lda + ch * 16);
+    }
 #pragma unroll
-  for (int i = 0; i < B_DMA; ++i) {
-    const int row = (i * NW + wave) * RPD + lane / CPR;
-    const int ch = (lane % CPR) ^ lds_swz<BK>(row);
-    b_off[i] = (uint32_t)((min(n0 + row, p.N - 1) - n0) * p.ldw + ch * 16);
-  }
+    for (int i = 0; i < B_DMA; ++i) {
+      const int row = (i * NW + wave) * RPD + lane / CPR;
+      const int ch = (lane % CPR) ^ lds_swz<BK>(row);
+      b_off[i] = (uint32_t)((min(n0 + row, p.N - 1) - n0) * p.ldw + ch * 16);
+    }
+  };
+  setup(tile);
   const uint32_t lds_wave =
       __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)D3_LDS_PTR(lds) + (uint32_t)wave * 1024u);
 
@@ -697,13 +747,6 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   auto dma_stage = [&](auto u_c, int kt) { static_for<0, DPS>([&](auto d_c) { dma_one(u_c, d_c, kt); }); };
 
   acc_t acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-
   frag_t fa[SUB][TM];     // A operands of the current step (single buffer)
   frag_t fb[2][SUB][TN];  // B operands, by step parity
 
@@ -787,47 +830,85 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   };
 
   // Prologue: DMA of steps 0..3 fills every stage; then the operands of step 0.
-  dma_stage(std::integral_constant<int, 0>{}, 0);
-  if (nk > 1) dma_stage(std::integral_constant<int, 1>{}, 1);
-  if (nk > 2) dma_stage(std::integral_constant<int, 2>{}, 2);
-  if (nk > 3) dma_stage(std::integral_constant<int, 3>{}, 3);
-  {
-    const int after = min(kStages - 1, nk - 1);  // DMA steps issued after step 0
-    if (after >= 3) wait_vmcnt<3 * DPS>();
-    else if (after == 2) wait_vmcnt<2 * DPS>();
-    else if (after == 1) wait_vmcnt<DPS>();
-    else wait_vmcnt<0>();
-  }
-  lds_barrier();
-  read_all(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+  auto prologue_dma = [&] {
+    dma_stage(std::integral_constant<int, 0>{}, 0);
+    if (nk > 1) dma_stage(std::integral_constant<int, 1>{}, 1);
+    if (nk > 2) dma_stage(std::integral_constant<int, 2>{}, 2);
+    if (nk > 3) dma_stage(std::integral_constant<int, 3>{}, 3);
+  };
+  prologue_dma();
+  bool first = true;
+  for (;;) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    if (first) {
+      const int after = min(kStages - 1, nk - 1);  // DMA steps issued after step 0
+      if (after >= 3) wait_vmcnt<3 * DPS>();
+      else if (after == 2) wait_vmcnt<2 * DPS>();
+      else if (after == 1) wait_vmcnt<DPS>();
+      else wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<0>();  // this tile's prologue DMA (issued in the last epilogue) and that epilogue's stores
+    }
+    first = false;
+    lds_barrier();
+    read_all(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
 
-  using Steady = std::integral_constant<bool, false>;
-  using Checked = std::integral_constant<bool, true>;
-  int kt0 = 0;
-  for (; kt0 + 2 * kStages <= nk; kt0 += 4) {
-    step(std::integral_constant<int, 0>{}, Steady{}, kt0);
-    step(std::integral_constant<int, 1>{}, Steady{}, kt0 + 1);
-    step(std::integral_constant<int, 2>{}, Steady{}, kt0 + 2);
-    step(std::integral_constant<int, 3>{}, Steady{}, kt0 + 3);
-  }
-  for (; kt0 < nk; kt0 += 4) {
-    step(std::integral_constant<int, 0>{}, Checked{}, kt0);
-    if (kt0 + 1 < nk) step(std::integral_constant<int, 1>{}, Checked{}, kt0 + 1);
-    if (kt0 + 2 < nk) step(std::integral_constant<int, 2>{}, Checked{}, kt0 + 2);
-    if (kt0 + 3 < nk) step(std::integral_constant<int, 3>{}, Checked{}, kt0 + 3);
-  }
+    using Steady = std::integral_constant<bool, false>;
+    using Checked = std::integral_constant<bool, true>;
+    int kt0 = 0;
+    for (; kt0 + 2 * kStages <= nk; kt0 += 4) {
+      step(std::integral_constant<int, 0>{}, Steady{}, kt0);
+      step(std::integral_constant<int, 1>{}, Steady{}, kt0 + 1);
+      step(std::integral_constant<int, 2>{}, Steady{}, kt0 + 2);
+      step(std::integral_constant<int, 3>{}, Steady{}, kt0 + 3);
+    }
+    for (; kt0 < nk; kt0 += 4) {
+      step(std::integral_constant<int, 0>{}, Checked{}, kt0);
+      if (kt0 + 1 < nk) step(std::integral_constant<int, 1>{}, Checked{}, kt0 + 1);
+      if (kt0 + 2 < nk) step(std::integral_constant<int, 2>{}, Checked{}, kt0 + 2);
+      if (kt0 + 3 < nk) step(std::integral_constant<int, 3>{}, Checked{}, kt0 + 3);
+    }
 
-  if constexpr (kSplitTile<BM, BN>) {
-    if (S > 1) {
-      splitk_store<MODE, NW, TM, TN>(p, acc, tm * p.tiles_n + tn, split, wave, lane);
+    if constexpr (kSplitTile<BM, BN>) {
+      if (S > 1) {
+        splitk_store<MODE, NW, TM, TN>(p, acc, tm * p.tiles_n + tn, split, wave, lane);
+        return;
+      }
+    }
+    // every wave has finished reading the stages (before they take the epilogue's rows, or the next
+    // tile's DMA)
+    wait_lgkm0();
+    lds_barrier();
+    if constexpr (PERSIST) {
+      const int next = tile + (int)gridDim.x;
+      const bool more = next < ntiles;  // uniform over the workgroup
+      const int64_t wrow0 = m0 + wm * WTM, wcol0 = n0 + wn * WTN;
+      static_assert(kStages * STAGE + NW * PL::E::BYTES <= (int)sizeof(lds), "epilogue staging");
+      epilogue<MODE, TM, TN, EPI, OUT, PL::PACK>(p, acc, wrow0, wcol0, lane, lds + kStages * STAGE + wave * PL::E::BYTES,
+                                                 [&] {
+                                                   if (more) {
+                                                     // the epilogue's scales have landed, so its later
+                                                     // waits do not cover this DMA
+                                                     asm volatile("" ::: "memory");
+                                                     wait_vmcnt<0>();
+                                                     setup(next);
+                                                     prologue_dma();
+                                                   }
+                                                 });
+      if (!more) return;
+      tile = next;
+    } else {
+      static_assert(NW * EpiLds<TN, EPI, OUT>::BYTES <= (int)sizeof(lds), "epilogue staging");
+      epilogue<MODE, TM, TN, EPI, OUT>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane,
+                                       lds + wave * EpiLds<TN, EPI, OUT>::BYTES);
       return;
     }
   }
-  // every wave has finished reading the stages before they hold the epilogue's rows
-  wait_lgkm0();
-  lds_barrier();
-  static_assert(NW * EpiLds<TN, EPI, OUT>::BYTES <= (int)sizeof(lds), "epilogue staging");
-  epilogue<MODE, TM, TN, EPI, OUT>(p, acc, m0 + wm * WTM, n0 + wn * WTN, lane, lds + wave * EpiLds<TN, EPI, OUT>::BYTES);
 }
 
 // ---------------------------------------------------------------------------
@@ -848,7 +929,13 @@ static hipError_t launch_dma(GemmParams p, hipStream_t st) {
   p.tiles_m = (int)((p.M + BM - 1) / BM);
   p.tiles_n = (int)((p.N + BN - 1) / BN);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
-  hipLaunchKernelGGL((gemm_w8a8_dma<MODE, BM, BN, WM, WN, EPI, OUT, BK>), dim3((unsigned)(tiles * p.ksplit)),
+  int64_t grid = tiles * p.ksplit;
+  if (PersistLayout<MODE, BM, BN, WM, WN, EPI, OUT, BK>::value && gemm_persistent()) {
+    // one workgroup per CU; a multiple of the 8 XCDs keeps each workgroup's tiles on its own XCD
+    const int64_t cus = device_cu_count() & ~7;
+    if (cus >= 8 && tiles > cus) grid = cus;
+  }
+  hipLaunchKernelGGL((gemm_w8a8_dma<MODE, BM, BN, WM, WN, EPI, OUT, BK>), dim3((unsigned)grid),
                      dim3(WM * WN * 64), 0, st, p);
   if (kSplitTile<BM, BN> && p.ksplit > 1) {
     const hipError_t e = hipGetLastError();

@@ -79,4 +79,11 @@ hipError_t launch_gemm(int mode, GemmParams p, int epi, int out_dt, const GemmPl
 
 constexpr int64_t kMaxVecK = 32 * 512;  // longest row the one-pass quant kernels hold in registers
 
+// Compute units of the current device (queried once per device).
+int device_cu_count();
+// Whether the pipelined GEMMs that can run persistently (one workgroup per CU
+// walking several tiles) do so: yes, unless D3W8A8_GEMM_PERSIST=0 is set in
+// the environment (read once; a measurement switch).
+bool gemm_persistent();
+
 }  // namespace d3
