@@ -15,6 +15,8 @@ the path, each timed on the GPU with HIP events on the launch stream:
                        launch per projection (K = 4096; N = 6144, 4096, 24576)
   mlp_block_int8       norm + quant -> gate_up + SwiGLU -> requant -> down + residual,
                        M = 4096, hidden 4096, intermediate 12288
+  gated_o_proj_quant_fp8  quantize_rows(out * sigmoid(gate)) fused, 4096 x 4096, the gate read in
+                       place from the q_proj output
   question_gemms_fp8_m128  the four projections at M = 128 (a batch of 8 question blocks),
                        weights streamed from HBM (pool > Infinity Cache): HBM GB/s
   linear_stack_fp8     48 layers of QKV / o_proj / MLP block, identity mixer: one
@@ -461,6 +463,35 @@ def run_mlp_block(args):
             "norm_gain": "N(1, 0.1) applied as (1 + w), w ~ N(0, 0.1)"}
 
 
+def run_gated_quant(args):
+    """The gated attention output projection's input, quantize_rows(out * sigmoid(gate)) fused
+    (core.py:297), at 4096 tokens x 4096: the gate read in place from the q_proj output [4096, 8192]
+    (head_dim 256), inputs rotated over > 256 MB (cold). HBM bytes: out and gate in, codes and scales out."""
+    import torch
+
+    from d3trt_amd import _lib
+    from d3trt_amd import kernels as KK
+
+    dev = torch.device("cuda:0")
+    M, K, hd = 4096, 4096, 256
+    g = torch.Generator(device=dev).manual_seed(0)
+    per = M * K * 2 * 3  # out + the q_proj output (query and gate halves)
+    n = max(2, -(-ROTATE_BYTES // per))
+    outs = [torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16) for _ in range(n)]
+    qps = [torch.randn(M, 2 * K, generator=g, device=dev).to(torch.bfloat16) for _ in range(n)]
+    q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty(M, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    us = launch_us(lambda i: _lib.check(lib.d3w8a8_gate_quantize(
+        KK.mode_code("fp8"), KK.dtype_code(torch.bfloat16), outs[i % n].data_ptr(), K, qps[i % n].data_ptr(),
+        2 * K, hd, M, K, q.data_ptr(), K, s.data_ptr(), None, 0, torch.cuda.current_stream().cuda_stream),
+        "gate_quantize"), 4 * n)
+    byts = M * K * 2 + M * K * 2 + M * K + 4 * M
+    return {"shape": f"{M}x{K}", "head_dim": hd, "us": round(us, 2), "gbs": round(byts / (us * 1e-6) / 1e9, 1),
+            "frac_hbm": round(byts / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "algo_bytes": byts, "note": "out and gate (in place in the q_proj output) in, e4m3 codes + scales out"}
+
+
 def run_linear_stack(args):
     """48-layer FP8 projection stack (identity mixer): state pass of 8192 tokens, then 255 question
     blocks of 16 tokens in ragged batches of 8 blocks and of all 255 blocks."""
@@ -646,7 +677,8 @@ def main() -> int:
     if not args.headline_only:
         configs = {}
         for name, fn in (("single_int8_linear", run_single_linear), ("ragged_int8", run_ragged),
-                         ("mlp_block_int8", run_mlp_block), ("question_gemms_fp8_m128", run_question_gemms),
+                         ("mlp_block_int8", run_mlp_block), ("gated_o_proj_quant_fp8", run_gated_quant),
+                         ("question_gemms_fp8_m128", run_question_gemms),
                          ("linear_stack_fp8", run_linear_stack)):
             configs[name] = fn(args)
             print(json.dumps({"progress": name, "done": True}), file=sys.stderr, flush=True)

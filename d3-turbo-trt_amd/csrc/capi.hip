@@ -93,6 +93,29 @@ int d3w8a8_quantize_rows_amax(int mode, int in_dtype, const void* h, int64_t ldh
                     "quantize_rows_amax");
 }
 
+int d3w8a8_gate_quantize(int mode, int in_dtype, const void* x, int64_t ldx, const void* gate, int64_t ldg,
+                         int64_t gate_head_dim, int64_t M, int64_t K, void* q, int64_t ldq, float* scale,
+                         void* y_out, int64_t ldy, void* stream) {
+  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "gate_quantize: unknown mode %d", mode);
+  if (in_dtype != D3W8A8_BF16 && in_dtype != D3W8A8_F16)
+    return fail(D3W8A8_EINVAL, "gate_quantize: inputs must be bf16 or fp16");
+  if (M < 0 || K < 8 || K % 8 != 0 || K > d3::kMaxVecK || ldx < K || ldq < K || (y_out && ldy < K))
+    return fail(D3W8A8_EINVAL, "gate_quantize: bad shape M=%lld K=%lld (K must be a multiple of 8, <= %lld)",
+                (long long)M, (long long)K, (long long)d3::kMaxVecK);
+  if (gate_head_dim < 0 || (gate_head_dim > 0 && (gate_head_dim % 8 != 0 || K % gate_head_dim != 0)))
+    return fail(D3W8A8_EINVAL, "gate_quantize: gate_head_dim must be 0 or a multiple of 8 dividing K");
+  if (ldg < (gate_head_dim > 0 ? 2 * K : K))
+    return fail(D3W8A8_EINVAL, "gate_quantize: ldg must cover the gate row (2 K for the q_proj layout)");
+  if (M == 0) return D3W8A8_OK;
+  if (!x || !gate || !q || !scale) return fail(D3W8A8_EINVAL, "gate_quantize: null pointer");
+  if ((ldx * 2) % 16 || (ldg * 2) % 16 || !aligned(x, 16) || !aligned(gate, 16) || ldq % 8 || !aligned(q, 8) ||
+      (y_out && ((ldy * 2) % 16 || !aligned(y_out, 16))))
+    return fail(D3W8A8_EINVAL, "gate_quantize: rows must be 16-byte aligned");
+  return hip_status(d3::launch_gate_quant(mode, in_dtype, x, ldx, gate, ldg, gate_head_dim, M, K, q, ldq, scale, y_out,
+                                          ldy, (hipStream_t)stream),
+                    "gate_quantize");
+}
+
 int d3w8a8_quantize_rows_ragged(int mode, int in_dtype, const void* x, int64_t ldx, const int32_t* lengths,
                                 int64_t nseg, int64_t width, int64_t K, void* q, int64_t ldq, float* scale,
                                 int32_t* row_map, void* out, int out_dtype, int64_t ldo, int64_t N, void* stream) {

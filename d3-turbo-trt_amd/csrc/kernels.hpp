@@ -37,6 +37,11 @@ hipError_t launch_quant_rows_amax(int mode, int dt, const void* h, int64_t ldh, 
 hipError_t launch_rmsnorm_quant(int mode, int dt, int dtw, const void* x, int64_t ldx, const void* w, int64_t M,
                                 int64_t K, float eps, int zc, void* q, int64_t ldq, float* scale, void* normed,
                                 int64_t ldn, float* clear_amax, hipStream_t st);
+// o_proj input of a gated attention layer: quantize_rows(x * sigmoid(gate)); head_dim > 0 reads the
+// gate in place from the per-head [query | gate] rows of the q_proj output. 16-bit inputs only.
+hipError_t launch_gate_quant(int mode, int dt, const void* x, int64_t ldx, const void* gate, int64_t ldg,
+                             int64_t head_dim, int64_t M, int64_t K, void* q, int64_t ldq, float* scale, void* y_out,
+                             int64_t ldy, hipStream_t st);
 // Packed-row offsets of a ragged batch, passed by value in the kernel arguments:
 // segment b owns packed rows [off[b], off[b + 1]).
 constexpr int kMaxSegments = 256;

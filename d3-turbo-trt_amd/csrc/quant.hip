@@ -134,6 +134,76 @@ __global__ __launch_bounds__(256) void quant_rows_amax_vec(const void* __restric
 }
 
 // ---------------------------------------------------------------------------
+// Gated o_proj input: y = DT( x * DT(sigmoid(gate)) ), then quantize_rows(y)
+// (d3trt/model/core.py:297: o_proj(out * torch.sigmoid(gate)); torch rounds
+// the sigmoid to the tensor dtype, then the product). The gate is either a
+// [M, K] tensor (head_dim == 0) or read in place from the q_proj output, whose
+// rows hold per head [query (head_dim) | gate (head_dim)] (core.py:231, the
+// chunk of the q_proj output viewed as [.., heads, 2 head_dim]): gate column k
+// sits at (k / head_dim) * 2 head_dim + head_dim + k % head_dim
+// (head_dim % 8 == 0, so an 8-element chunk never straddles two heads).
+// One wave per row; optional y output (the bf16 product).
+// ---------------------------------------------------------------------------
+template <int MODE, int DT, int NCH, bool FULL>
+__global__ __launch_bounds__(256) void gate_quant_vec(const void* __restrict__ x, int64_t ldx,
+                                                     const void* __restrict__ gate, int64_t ldg, int64_t head_dim,
+                                                     int64_t M, int64_t K, void* __restrict__ q, int64_t ldq,
+                                                     float* __restrict__ scale, void* __restrict__ y_out,
+                                                     int64_t ldy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+  if (row >= M) return;
+  using RC = RowChunks<DT, NCH, FULL>;
+  RC x_, g_;
+  x_.load((const char*)x + row * ldx * RC::kES, K, lane);
+  {
+    const char* grow = (const char*)gate + row * ldg * RC::kES;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int64_t k = FULL ? RC::col(c, lane) : min(RC::col(c, lane), K - 8);
+      const int64_t gk = head_dim ? (k / head_dim) * 2 * head_dim + head_dim + k % head_dim : k;
+      const uint4 t = *(const uint4*)(grow + gk * RC::kES);
+      g_.w[c][0] = t.x;
+      g_.w[c][1] = t.y;
+      g_.w[c][2] = t.z;
+      g_.w[c][3] = t.w;
+    }
+  }
+  RC y;
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (RC::valid(c, lane, K)) {
+      float v[8], gv[8];
+      x_.get(c, v);
+      g_.get(c, gv);
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        float s0 = 1.0f / (1.0f + expf(-gv[i]));
+        float s1 = 1.0f / (1.0f + expf(-gv[i + 1]));
+        round_pair_to<DT>(s0, s1);  // torch.sigmoid's output in the tensor dtype
+        float p0 = v[i] * s0, p1 = v[i + 1] * s1;
+        y.put_pair(c, i / 2, p0, p1);
+        amax = fmaxf(fmaxf(amax, fabsf(p0)), fabsf(p1));
+      }
+    }
+  }
+  const RowScale s = scale_from_amax<MODE>(wave_max(amax));
+  char* qr = (char*)q + row * ldq;
+  char* yr = y_out ? (char*)y_out + row * ldy * RC::kES : nullptr;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (RC::valid(c, lane, K)) {
+      float v[8];
+      y.get(c, v);
+      quant_store8<MODE>(qr + RC::col(c, lane), v, s);
+      if (yr) y.store_raw(c, yr + RC::col(c, lane) * RC::kES);
+    }
+  }
+  if (lane == 0) scale[row] = s.s;
+}
+
+// ---------------------------------------------------------------------------
 // Ragged gather: x is the right-padded [nseg, width, K] question batch;
 // segment b holds off[b+1] - off[b] valid rows. Valid row (b, t) is quantized
 // into packed row off[b] + t and row_map[packed] = b * width + t. Padded rows
@@ -226,6 +296,27 @@ hipError_t launch_quant_rows_amax(int mode, int dt, const void* h, int64_t ldh, 
 #define C(MO, D) if (mode == MO && dt == D) return launch_quant_rows_amax_t<MO, D>(h, ldh, amax, M, K, q, ldq, scale, st)
   C(kInt8, kBF16); C(kInt8, kF16); C(kInt8, kF32);
   C(kFp8, kBF16); C(kFp8, kF16); C(kFp8, kF32);
+#undef C
+  return hipErrorInvalidValue;
+}
+
+template <int MODE, int DT>
+hipError_t launch_gate_quant_t(const void* x, int64_t ldx, const void* gate, int64_t ldg, int64_t head_dim, int64_t M,
+                               int64_t K, void* q, int64_t ldq, float* scale, void* y_out, int64_t ldy,
+                               hipStream_t st) {
+  if (M == 0) return hipSuccess;
+#define L(N, F) hipLaunchKernelGGL((gate_quant_vec<MODE, DT, N, F>), quant_grid(M), dim3(256), 0, st, x, ldx, gate, ldg, head_dim, M, K, q, ldq, scale, y_out, ldy)
+  D3_NCH_DISPATCH(K, L);
+#undef L
+  return hipGetLastError();
+}
+
+hipError_t launch_gate_quant(int mode, int dt, const void* x, int64_t ldx, const void* gate, int64_t ldg,
+                             int64_t head_dim, int64_t M, int64_t K, void* q, int64_t ldq, float* scale, void* y_out,
+                             int64_t ldy, hipStream_t st) {
+  if (K > kMaxVecK) return hipErrorInvalidValue;
+#define C(MO, D) if (mode == MO && dt == D) return launch_gate_quant_t<MO, D>(x, ldx, gate, ldg, head_dim, M, K, q, ldq, scale, y_out, ldy, st)
+  C(kInt8, kBF16); C(kInt8, kF16); C(kFp8, kBF16); C(kFp8, kF16);
 #undef C
   return hipErrorInvalidValue;
 }

@@ -113,6 +113,34 @@ def quantize_rows_amax(h: torch.Tensor, amax: torch.Tensor, mode: str):
     return q, s
 
 
+def gate_quantize(x: torch.Tensor, gate: torch.Tensor, mode: str, *, gate_head_dim: int = 0,
+                  want_y: bool = False):
+    """quantize_rows(x * sigmoid(gate)) fused: the o_proj input of a gated attention layer (core.py:297).
+
+    ``gate`` is [M, K] (``gate_head_dim=0``), or the q_proj output [M, 2K] whose rows hold per head
+    [query (head_dim) | gate (head_dim)] (core.py:231), read in place with ``gate_head_dim=head_dim``.
+    Returns (q [M, K], scale [M, 1], y or None), y = the product in x's dtype.
+    """
+    x = _rows(x, "x")
+    gate = _rows(gate, "gate")
+    M, K = x.shape
+    want_cols = 2 * K if gate_head_dim else K
+    if gate.shape != (M, want_cols):
+        raise ValueError(f"gate shape {tuple(gate.shape)} does not match x {tuple(x.shape)} "
+                         f"(expected [{M}, {want_cols}])")
+    if gate.dtype != x.dtype:
+        raise ValueError("gate and x must share a dtype")
+    q = torch.empty(M, K, dtype=qdtype(mode), device=x.device)
+    s = torch.empty(M, 1, dtype=torch.float32, device=x.device)
+    y = torch.empty(M, K, dtype=x.dtype, device=x.device) if want_y else None
+    lib = _lib.load()
+    rc = lib.d3w8a8_gate_quantize(mode_code(mode), dtype_code(x.dtype), x.data_ptr(), x.stride(0), gate.data_ptr(),
+                                  gate.stride(0), int(gate_head_dim), M, K, q.data_ptr(), K, s.data_ptr(), _ptr(y),
+                                  K if y is not None else 0, _stream(x))
+    _lib.check(rc, "gate_quantize")
+    return q, s, y
+
+
 def quantize_rows_ragged(x: torch.Tensor, lengths: Sequence[int], mode: str, *,
                          out: Optional[torch.Tensor] = None):
     """Right-padded [B, W, K] -> packed (q [T, K], scale [T, 1], row_map [T] int32), T = sum(lengths).

@@ -157,6 +157,22 @@ class QuantLinear(nn.Module):
         self.kernel = self._kernel_name()
         return out.reshape(*shape, self.out_features)
 
+    def forward_gated(self, x: torch.Tensor, gate: torch.Tensor, *, gate_head_dim: int = 0) -> torch.Tensor:
+        """``forward(x * torch.sigmoid(gate))`` with the product fused into the quantization: the gated
+        attention output projection, ``attn.o_proj(out * torch.sigmoid(gate))`` (core.py:297).
+
+        ``gate`` has x's shape, or (``gate_head_dim=head_dim``) is the q_proj output, [..., 2 * in], whose
+        rows hold per head [query | gate] (core.py:231); the gate half is then read in place.
+        """
+        shape = x.shape[:-1]
+        flat = x.reshape(-1, self.in_features)
+        g = gate.reshape(flat.shape[0], -1)
+        q, scale, _ = K.gate_quantize(flat, g, self.mode, gate_head_dim=gate_head_dim)
+        out = K.gemm(self.mode, q, scale.reshape(-1), self.weight, self.weight_scale,
+                     epilogue=_lib.EPI_DEQUANT, out_dtype=self.dtype)
+        self.kernel = self._kernel_name()
+        return out.reshape(*shape, self.out_features)
+
     def forward_ragged(self, x: torch.Tensor, lengths: Sequence[int]) -> torch.Tensor:
         """A right-padded question batch [B, W, in] with ``lengths[b]`` valid rows per block.
 

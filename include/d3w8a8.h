@@ -88,6 +88,16 @@ int d3w8a8_rmsnorm_quantize(int mode, int in_dtype, const void* x, int64_t ldx, 
 int d3w8a8_quantize_rows_amax(int mode, int in_dtype, const void* h, int64_t ldh, const float* amax,
                               int64_t M, int64_t K, void* q, int64_t ldq, float* scale, void* stream);
 
+/* o_proj input of a gated attention layer, quantized per token: y = OUT(x * OUT(sigmoid(gate))), then
+ * quantize_rows(y). Replaces `attn.o_proj(out * torch.sigmoid(gate))`'s elementwise product and
+ * quantize (d3trt/model/core.py:297 with quant.py:92-100). x [M, K] (ld ldx), bf16 or fp16.
+ * gate_head_dim == 0: gate is [M, K] (ld ldg >= K). gate_head_dim > 0 (a multiple of 8 dividing K):
+ * gate is read in place from the q_proj output [M, 2K] (ld ldg >= 2K), whose rows hold per head
+ * [query (head_dim) | gate (head_dim)] (core.py:231). y_out (optional, ld ldy): the product. */
+int d3w8a8_gate_quantize(int mode, int in_dtype, const void* x, int64_t ldx, const void* gate, int64_t ldg,
+                         int64_t gate_head_dim, int64_t M, int64_t K, void* q, int64_t ldq, float* scale,
+                         void* y_out, int64_t ldy, void* stream);
+
 /* Ragged gather-quantize for a right-padded question batch x [nseg, width, K]
  * (backends/trtllm.py:149-179 builds such batches; core.py:158-181 runs them):
  * valid row (b, t < lengths[b]) is quantized into packed row off(b) + t with

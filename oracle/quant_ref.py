@@ -220,6 +220,21 @@ def swiglu(gate_up: torch.Tensor) -> torch.Tensor:
     return F.silu(gate) * up
 
 
+def split_query_gate(q_proj_out: torch.Tensor, head_dim: int):
+    """D3Core._attention's split of the q_proj output (core.py:231-232): rows viewed as
+    [heads, 2 * head_dim], chunked into query and gate halves, the gate reshaped to [..., heads * head_dim]."""
+    t = _cpu(q_proj_out)
+    shape = t.shape[:-1]
+    query, gate = torch.chunk(t.view(*shape, -1, head_dim * 2), 2, dim=-1)
+    return query, gate.reshape(*shape, -1)
+
+
+def gated_input(out: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+    """The o_proj input of a gated attention layer, ``out * torch.sigmoid(gate)`` (core.py:297), in the
+    tensors' dtype: torch rounds the sigmoid to that dtype, then the product."""
+    return _cpu(out) * torch.sigmoid(_cpu(gate))
+
+
 def mlp_block(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
               wgu_q: torch.Tensor, wgu_s: torch.Tensor,
               wd_q: torch.Tensor, wd_s: torch.Tensor, mode: str,

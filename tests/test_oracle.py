@@ -223,6 +223,33 @@ def test_swiglu_closed_form_and_halves():
     assert not torch.equal(h, swapped)
 
 
+def test_gated_input_known_answers_and_closed_form():
+    """core.py:297, out * sigmoid(gate): sigmoid(0) = 1/2 exactly, saturation at |gate| = 30, and the
+    float64 closed form within two bf16 roundings (sigmoid rounded, then the product)."""
+    g = gen(21)
+    out = (torch.randn(5, 96, generator=g) * 4).to(torch.bfloat16)
+    half = R.gated_input(out, torch.zeros_like(out))
+    assert torch.equal(half, (out.double() / 2).to(torch.bfloat16))
+    assert torch.equal(R.gated_input(out, torch.full_like(out, 30.0)), out)
+    assert float(R.gated_input(out, torch.full_like(out, -30.0)).abs().max()) < 1e-11 * float(out.abs().max())
+    gate = (torch.randn(5, 96, generator=g) * 3).to(torch.bfloat16)
+    y = R.gated_input(out, gate)
+    exact = out.double() / (1 + torch.exp(-gate.double()))
+    assert torch.all((y.double() - exact).abs() <= exact.abs() * 2.0 ** -7 + 1e-30)
+    # the gate is the sigmoid's argument, not the product's other factor
+    assert not torch.equal(y, R.gated_input(gate, out))
+
+
+def test_split_query_gate_takes_the_second_half_of_each_head():
+    """core.py:231-232: q_proj rows viewed as [heads, 2 head_dim]; the gate is each head's second half."""
+    heads, hd = 3, 8
+    row = torch.arange(2 * heads * hd, dtype=torch.float32)
+    query, gate = R.split_query_gate(row.reshape(1, -1).to(torch.bfloat16), hd)
+    want = torch.cat([row[h * 2 * hd + hd:(h + 1) * 2 * hd] for h in range(heads)])
+    assert torch.equal(gate.float().reshape(-1), want)
+    assert torch.equal(query.float().reshape(-1), torch.cat([row[h * 2 * hd:h * 2 * hd + hd] for h in range(heads)]))
+
+
 def test_outlier_generator_draw_order():
     g = gen(0)
     x = R.outlier_activations(g, 128, 1024)
