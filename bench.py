@@ -17,6 +17,7 @@ the path, each timed on the GPU with HIP events on the launch stream:
                        M = 4096, hidden 4096, intermediate 12288
   gated_o_proj_quant_fp8  quantize_rows(out * sigmoid(gate)) fused, 4096 x 4096, the gate read in
                        place from the q_proj output
+  gdn_norm_quant_fp8   gated RMSNorm over 32 heads of 128 + quantize fused, 4096 x 4096
   question_gemms_fp8_m128  the four projections at M = 128 (a batch of 8 question blocks),
                        weights streamed from HBM (pool > Infinity Cache): HBM GB/s
   linear_stack_fp8     48 layers of QKV / o_proj / MLP block, identity mixer: one
@@ -492,6 +493,35 @@ def run_gated_quant(args):
             "algo_bytes": byts, "note": "out and gate (in place in the q_proj output) in, e4m3 codes + scales out"}
 
 
+def run_gdn_norm_quant(args):
+    """The GDN output projection's input: Qwen3_5RMSNormGated over 32 heads of 128 fused with the per-token
+    quantize (core.py:390-391), 4096 tokens x 4096, inputs rotated over > 256 MB (cold). HBM bytes: the
+    core output and z in, codes and scales out."""
+    import torch
+
+    from d3trt_amd import _lib
+    from d3trt_amd import kernels as KK
+
+    dev = torch.device("cuda:0")
+    M, K, hd = 4096, 4096, 128
+    g = torch.Generator(device=dev).manual_seed(0)
+    n = max(2, -(-ROTATE_BYTES // (M * K * 2 * 2)))
+    xs = [torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16) for _ in range(n)]
+    zs = [torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16) for _ in range(n)]
+    w = (1 + 0.1 * torch.randn(hd, generator=g, device=dev)).to(torch.bfloat16)
+    q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty(M, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    us = launch_us(lambda i: _lib.check(lib.d3w8a8_gdn_norm_quantize(
+        KK.mode_code("fp8"), KK.dtype_code(torch.bfloat16), xs[i % n].data_ptr(), K, zs[i % n].data_ptr(), K,
+        KK.dtype_code(w.dtype), w.data_ptr(), hd, 1e-6, M, K, q.data_ptr(), K, s.data_ptr(), None, 0,
+        torch.cuda.current_stream().cuda_stream), "gdn_norm_quantize"), 4 * n)
+    byts = 2 * M * K * 2 + M * K + 4 * M + 2 * hd
+    return {"shape": f"{M}x{K}", "heads": K // hd, "head_dim": hd, "us": round(us, 2),
+            "gbs": round(byts / (us * 1e-6) / 1e9, 1), "frac_hbm": round(byts / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "algo_bytes": byts}
+
+
 def run_linear_stack(args):
     """48-layer FP8 projection stack (identity mixer): state pass of 8192 tokens, then 255 question
     blocks of 16 tokens in ragged batches of 8 blocks and of all 255 blocks."""
@@ -678,6 +708,7 @@ def main() -> int:
         configs = {}
         for name, fn in (("single_int8_linear", run_single_linear), ("ragged_int8", run_ragged),
                          ("mlp_block_int8", run_mlp_block), ("gated_o_proj_quant_fp8", run_gated_quant),
+                         ("gdn_norm_quant_fp8", run_gdn_norm_quant),
                          ("question_gemms_fp8_m128", run_question_gemms),
                          ("linear_stack_fp8", run_linear_stack)):
             configs[name] = fn(args)

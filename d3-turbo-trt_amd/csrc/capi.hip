@@ -116,6 +116,30 @@ int d3w8a8_gate_quantize(int mode, int in_dtype, const void* x, int64_t ldx, con
                     "gate_quantize");
 }
 
+int d3w8a8_gdn_norm_quantize(int mode, int in_dtype, const void* x, int64_t ldx, const void* z, int64_t ldz,
+                             int w_dtype, const void* w, int64_t head_dim, float eps, int64_t M, int64_t K, void* q,
+                             int64_t ldq, float* scale, void* y_out, int64_t ldy, void* stream) {
+  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "gdn_norm_quantize: unknown mode %d", mode);
+  if (in_dtype != D3W8A8_BF16 && in_dtype != D3W8A8_F16)
+    return fail(D3W8A8_EINVAL, "gdn_norm_quantize: inputs must be bf16 or fp16");
+  if (w_dtype != in_dtype && w_dtype != D3W8A8_F32)
+    return fail(D3W8A8_EINVAL, "gdn_norm_quantize: weight dtype must be fp32 or the input dtype");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256 && head_dim != 512)
+    return fail(D3W8A8_EINVAL, "gdn_norm_quantize: head_dim must be 64, 128, 256 or 512");
+  if (M < 0 || K < head_dim || K % head_dim != 0 || K > d3::kMaxVecK || ldx < K || ldz < K || ldq < K ||
+      (y_out && ldy < K))
+    return fail(D3W8A8_EINVAL, "gdn_norm_quantize: bad shape M=%lld K=%lld (whole heads, K <= %lld)", (long long)M,
+                (long long)K, (long long)d3::kMaxVecK);
+  if (M == 0) return D3W8A8_OK;
+  if (!x || !z || !w || !q || !scale) return fail(D3W8A8_EINVAL, "gdn_norm_quantize: null pointer");
+  if ((ldx * 2) % 16 || (ldz * 2) % 16 || !aligned(x, 16) || !aligned(z, 16) || !aligned(w, 16) || ldq % 8 ||
+      !aligned(q, 8) || (y_out && ((ldy * 2) % 16 || !aligned(y_out, 16))))
+    return fail(D3W8A8_EINVAL, "gdn_norm_quantize: rows must be 16-byte aligned");
+  return hip_status(d3::launch_gdn_norm_quant(mode, in_dtype, w_dtype, x, ldx, z, ldz, w, (int)head_dim, eps, M, K, q,
+                                              ldq, scale, y_out, ldy, (hipStream_t)stream),
+                    "gdn_norm_quantize");
+}
+
 int d3w8a8_quantize_rows_ragged(int mode, int in_dtype, const void* x, int64_t ldx, const int32_t* lengths,
                                 int64_t nseg, int64_t width, int64_t K, void* q, int64_t ldq, float* scale,
                                 int32_t* row_map, void* out, int out_dtype, int64_t ldo, int64_t N, void* stream) {

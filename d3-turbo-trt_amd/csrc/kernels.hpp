@@ -42,6 +42,11 @@ hipError_t launch_rmsnorm_quant(int mode, int dt, int dtw, const void* x, int64_
 hipError_t launch_gate_quant(int mode, int dt, const void* x, int64_t ldx, const void* gate, int64_t ldg,
                              int64_t head_dim, int64_t M, int64_t K, void* q, int64_t ldq, float* scale, void* y_out,
                              int64_t ldy, hipStream_t st);
+// GDN output: gated RMSNorm over heads of head_dim (64, 128, 256 or 512), then quantize_rows over the
+// whole row. 16-bit inputs; w is head_dim entries of the input dtype or fp32.
+hipError_t launch_gdn_norm_quant(int mode, int dt, int dtw, const void* x, int64_t ldx, const void* z, int64_t ldz,
+                                 const void* w, int head_dim, float eps, int64_t M, int64_t K, void* q, int64_t ldq,
+                                 float* scale, void* y_out, int64_t ldy, hipStream_t st);
 // Packed-row offsets of a ragged batch, passed by value in the kernel arguments:
 // segment b owns packed rows [off[b], off[b + 1]).
 constexpr int kMaxSegments = 256;

@@ -136,6 +136,120 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
       });
 }
 
+// ---------------------------------------------------------------------------
+// GDN output: gated RMSNorm over heads of head_dim, then the per-token quantize
+// of out_proj's input (d3trt/model/core.py:390-391: delta.norm(core, z) on rows
+// of head_v_dim, reshaped back to [tokens, heads * head_v_dim]; the norm is
+// transformers' Qwen3_5RMSNormGated, modeling_qwen3_5.py:168-184, built in the
+// model dtype, trtllm_stack.py:198):
+//   h = x * rstd_head  (fp32; rstd = 1 / sqrt(mean over the head of x^2 + eps))
+//   h = w * DT(h)      (rounded to DT when w is DT; fp32 when w is fp32)
+//   y = DT( h * silu(z) ),  silu(z) = z / (1 + exp(-z)) in fp32
+// then q(y) per token over the whole row. w has head_dim entries, shared by the
+// heads. head_dim divides 512 (64, 128, 256, 512): the 8-element pieces of one
+// head sit in head_dim / 8 consecutive lanes of one chunk, whose sum of squares
+// is an xor butterfly over those lanes (every lane of the group ends with the
+// same sum: each step adds the same two values). One wave per row.
+// ---------------------------------------------------------------------------
+template <int MODE, int DT, int DTW, int NCH, bool FULL>
+__global__ __launch_bounds__(256) void gdn_norm_quant_vec(
+    const void* __restrict__ x, int64_t ldx, const void* __restrict__ z, int64_t ldz, const void* __restrict__ w,
+    int head_dim, float eps, int64_t M, int64_t K, void* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+    void* __restrict__ y_out, int64_t ldy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
+  if (row >= M) return;
+  using RC = RowChunks<DT, NCH, FULL>;
+  RC x_, z_;
+  x_.load((const char*)x + row * ldx * RC::kES, K, lane);
+  z_.load((const char*)z + row * ldz * RC::kES, K, lane);
+  // this lane's 8 weights: columns 512 c + 8 lane of every chunk fall on head offset (8 lane) % head_dim
+  float wv[8];
+  {
+    using RW = RowChunks<DTW, 1, true>;
+    RW wp;
+    const uint4* src = (const uint4*)((const char*)w + (int64_t)((8 * lane) % head_dim) * RW::kES);
+#pragma unroll
+    for (int u = 0; u < RW::kWords / 4; ++u) {
+      const uint4 t = src[u];
+      wp.w[0][4 * u] = t.x;
+      wp.w[0][4 * u + 1] = t.y;
+      wp.w[0][4 * u + 2] = t.z;
+      wp.w[0][4 * u + 3] = t.w;
+    }
+    wp.get(0, wv);
+  }
+  const int group = head_dim >> 3;  // lanes per head
+  RC y;
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    // every lane of the wave takes part in the butterfly; lanes past the row contribute nothing used
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss = dot2_sq<DT>(x_.w[c][i], ss);
+    for (int off = 1; off < group; off <<= 1) ss = ss + __shfl_xor(ss, off, 64);
+    if (RC::valid(c, lane, K)) {
+      const float var = ss / (float)head_dim;
+      const float t = var + eps;
+      const float rstd = 1.0f / sqrtf(t);  // torch.rsqrt on the CPU: 1 / sqrt(t), each step correctly rounded
+      float v[8], zv[8];
+      x_.get(c, v);
+      z_.get(c, zv);
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        float h0 = v[i] * rstd, h1 = v[i + 1] * rstd;
+        round_pair_to<DT>(h0, h1);  // h.to(input_dtype)
+        h0 = wv[i] * h0;
+        h1 = wv[i + 1] * h1;
+        if constexpr (DTW == DT) round_pair_to<DT>(h0, h1);  // w (DT) * h (DT) is a DT tensor
+        const float e0 = expf(-zv[i]), e1 = expf(-zv[i + 1]);
+        const float d0 = 1.0f + e0, d1 = 1.0f + e1;
+        const float s0 = zv[i] / d0, s1 = zv[i + 1] / d1;
+        float p0 = h0 * s0, p1 = h1 * s1;
+        y.put_pair(c, i / 2, p0, p1);
+        amax = fmaxf(fmaxf(amax, fabsf(p0)), fabsf(p1));
+      }
+    }
+  }
+  const RowScale s = scale_from_amax<MODE>(wave_max(amax));
+  if constexpr (NCH > 12) y.fence();
+  char* qr = (char*)q + row * ldq;
+  char* yr = y_out ? (char*)y_out + row * ldy * RC::kES : nullptr;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (RC::valid(c, lane, K)) {
+      float v[8];
+      y.get(c, v);
+      quant_store8<MODE>(qr + RC::col(c, lane), v, s);
+      if (yr) y.store_raw(c, yr + RC::col(c, lane) * RC::kES);
+    }
+  }
+  if (lane == 0) scale[row] = s.s;
+}
+
+template <int MODE, int DT, int DTW>
+hipError_t launch_gdn_norm_quant_t(const void* x, int64_t ldx, const void* z, int64_t ldz, const void* w,
+                                   int head_dim, float eps, int64_t M, int64_t K, void* q, int64_t ldq, float* scale,
+                                   void* y_out, int64_t ldy, hipStream_t st) {
+  if (M == 0) return hipSuccess;
+#define L(N, F) hipLaunchKernelGGL((gdn_norm_quant_vec<MODE, DT, DTW, N, F>), quant_grid(M), dim3(256), 0, st, x, ldx, z, ldz, w, head_dim, eps, M, K, q, ldq, scale, y_out, ldy)
+  D3_NCH_DISPATCH(K, L);
+#undef L
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_norm_quant(int mode, int dt, int dtw, const void* x, int64_t ldx, const void* z, int64_t ldz,
+                                 const void* w, int head_dim, float eps, int64_t M, int64_t K, void* q, int64_t ldq,
+                                 float* scale, void* y_out, int64_t ldy, hipStream_t st) {
+  if (K > kMaxVecK) return hipErrorInvalidValue;
+#define C(MO, D, W) if (mode == MO && dt == D && dtw == W) return launch_gdn_norm_quant_t<MO, D, W>(x, ldx, z, ldz, w, head_dim, eps, M, K, q, ldq, scale, y_out, ldy, st)
+  C(kInt8, kBF16, kBF16); C(kInt8, kBF16, kF32); C(kInt8, kF16, kF16); C(kInt8, kF16, kF32);
+  C(kFp8, kBF16, kBF16); C(kFp8, kBF16, kF32); C(kFp8, kF16, kF16); C(kFp8, kF16, kF32);
+#undef C
+  return hipErrorInvalidValue;
+}
+
 template <int MODE, int DT, int DTW>
 hipError_t launch_rmsnorm_quant_t(const void* x, int64_t ldx, const void* w, int64_t M, int64_t K, float eps,
                                   int zc, void* q, int64_t ldq, float* scale, void* normed, int64_t ldn,

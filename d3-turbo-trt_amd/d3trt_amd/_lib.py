@@ -45,6 +45,8 @@ SIGNATURES = {
     "d3w8a8_rmsnorm_quantize": [_i32, _i32, _p, _i64, _i32, _p, _i64, _i64, _f32, _i32, _p, _i64, _p, _p,
                                 _i64, _p, _p],
     "d3w8a8_quantize_rows_amax": [_i32, _i32, _p, _i64, _p, _i64, _i64, _p, _i64, _p, _p],
+    "d3w8a8_gdn_norm_quantize": [_i32, _i32, _p, _i64, _p, _i64, _i32, _p, _i64, _f32, _i64, _i64, _p, _i64, _p,
+                                 _p, _i64, _p],
     "d3w8a8_gate_quantize": [_i32, _i32, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _p],
     "d3w8a8_quantize_rows_ragged": [_i32, _i32, _p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i32,
                                     _i64, _i64, _p],

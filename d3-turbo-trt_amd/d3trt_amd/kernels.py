@@ -141,6 +141,31 @@ def gate_quantize(x: torch.Tensor, gate: torch.Tensor, mode: str, *, gate_head_d
     return q, s, y
 
 
+def gdn_norm_quantize(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float, head_dim: int,
+                      mode: str, *, want_y: bool = False):
+    """Qwen3_5RMSNormGated over heads of ``head_dim`` (``delta.norm(core, z)``, core.py:390) fused with the
+    per-token quantize of out_proj's input. x, z [M, heads * head_dim]; weight [head_dim].
+    Returns (q [M, K], scale [M, 1], y or None), y = the normed, gated rows in x's dtype."""
+    x = _rows(x, "x")
+    z = _rows(z, "z")
+    M, K = x.shape
+    if z.shape != x.shape or z.dtype != x.dtype:
+        raise ValueError(f"z {tuple(z.shape)} {z.dtype} must match x {tuple(x.shape)} {x.dtype}")
+    w = _gpu(weight, "weight").contiguous()
+    if w.shape != (head_dim,):
+        raise ValueError(f"norm weight shape {tuple(w.shape)} does not match head_dim {head_dim}")
+    q = torch.empty(M, K, dtype=qdtype(mode), device=x.device)
+    s = torch.empty(M, 1, dtype=torch.float32, device=x.device)
+    y = torch.empty(M, K, dtype=x.dtype, device=x.device) if want_y else None
+    lib = _lib.load()
+    rc = lib.d3w8a8_gdn_norm_quantize(mode_code(mode), dtype_code(x.dtype), x.data_ptr(), x.stride(0),
+                                      z.data_ptr(), z.stride(0), dtype_code(w.dtype), w.data_ptr(), int(head_dim),
+                                      float(eps), M, K, q.data_ptr(), K, s.data_ptr(), _ptr(y),
+                                      K if y is not None else 0, _stream(x))
+    _lib.check(rc, "gdn_norm_quantize")
+    return q, s, y
+
+
 def quantize_rows_ragged(x: torch.Tensor, lengths: Sequence[int], mode: str, *,
                          out: Optional[torch.Tensor] = None):
     """Right-padded [B, W, K] -> packed (q [T, K], scale [T, 1], row_map [T] int32), T = sum(lengths).

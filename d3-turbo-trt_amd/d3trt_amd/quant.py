@@ -173,6 +173,19 @@ class QuantLinear(nn.Module):
         self.kernel = self._kernel_name()
         return out.reshape(*shape, self.out_features)
 
+    def forward_gated_norm(self, x: torch.Tensor, z: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                           head_dim: int) -> torch.Tensor:
+        """``forward(norm(x, z))`` with the gated RMSNorm over heads of ``head_dim`` fused into the
+        quantization: the GDN output projection, ``delta.out_proj(delta.norm(core, z))``
+        (core.py:390-391; the norm is Qwen3_5RMSNormGated with weight ``norm_weight``)."""
+        shape = x.shape[:-1]
+        flat = x.reshape(-1, self.in_features)
+        q, scale, _ = K.gdn_norm_quantize(flat, z.reshape(flat.shape), norm_weight, eps, head_dim, self.mode)
+        out = K.gemm(self.mode, q, scale.reshape(-1), self.weight, self.weight_scale,
+                     epilogue=_lib.EPI_DEQUANT, out_dtype=self.dtype)
+        self.kernel = self._kernel_name()
+        return out.reshape(*shape, self.out_features)
+
     def forward_ragged(self, x: torch.Tensor, lengths: Sequence[int]) -> torch.Tensor:
         """A right-padded question batch [B, W, in] with ``lengths[b]`` valid rows per block.
 

@@ -98,6 +98,17 @@ int d3w8a8_gate_quantize(int mode, int in_dtype, const void* x, int64_t ldx, con
                          int64_t gate_head_dim, int64_t M, int64_t K, void* q, int64_t ldq, float* scale,
                          void* y_out, int64_t ldy, void* stream);
 
+/* GDN output projection's input, quantized per token: Qwen3_5RMSNormGated over heads of head_dim
+ * (`delta.norm(core, z)`, d3trt/model/core.py:390-391; transformers modeling_qwen3_5.py:168-184, built
+ * in the model dtype, trtllm_stack.py:198), then quantize_rows over the whole row (quant.py:92-100):
+ *   h = x * rsqrt(mean_head(x^2) + eps) (fp32); h = w * IN(h) (rounded to IN when w is IN);
+ *   y = IN(h * silu(z)); q(y).
+ * x, z [M, K] (K = heads * head_dim), bf16 or fp16; w [head_dim] of the input dtype or fp32, shared by
+ * the heads; head_dim 64, 128, 256 or 512. y_out (optional, ld ldy): the normed, gated rows. */
+int d3w8a8_gdn_norm_quantize(int mode, int in_dtype, const void* x, int64_t ldx, const void* z, int64_t ldz,
+                             int w_dtype, const void* w, int64_t head_dim, float eps, int64_t M, int64_t K, void* q,
+                             int64_t ldq, float* scale, void* y_out, int64_t ldy, void* stream);
+
 /* Ragged gather-quantize for a right-padded question batch x [nseg, width, K]
  * (backends/trtllm.py:149-179 builds such batches; core.py:158-181 runs them):
  * valid row (b, t < lengths[b]) is quantized into packed row off(b) + t with

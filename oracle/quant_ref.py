@@ -220,6 +220,23 @@ def swiglu(gate_up: torch.Tensor) -> torch.Tensor:
     return F.silu(gate) * up
 
 
+def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float,
+                  head_dim: int) -> torch.Tensor:
+    """``delta.norm(core, z)`` of D3Core._delta (core.py:390): Qwen3_5RMSNormGated (transformers
+    modeling_qwen3_5.py:175-184) on rows of ``head_dim``, the module built in the model dtype
+    (trtllm_stack.py:198), reshaped back to x's shape."""
+    shape = x.shape
+    h = _cpu(x).reshape(-1, head_dim)
+    g = _cpu(z).reshape(-1, head_dim)
+    input_dtype = h.dtype
+    hs = h.to(torch.float32)
+    variance = hs.pow(2).mean(-1, keepdim=True)
+    hs = hs * torch.rsqrt(variance + eps)
+    hs = _cpu(weight) * hs.to(input_dtype)
+    hs = hs * F.silu(g.to(torch.float32))
+    return hs.to(input_dtype).reshape(shape)
+
+
 def split_query_gate(q_proj_out: torch.Tensor, head_dim: int):
     """D3Core._attention's split of the q_proj output (core.py:231-232): rows viewed as
     [heads, 2 * head_dim], chunked into query and gate halves, the gate reshaped to [..., heads * head_dim]."""

@@ -240,6 +240,31 @@ def test_gated_input_known_answers_and_closed_form():
     assert not torch.equal(y, R.gated_input(gate, out))
 
 
+@pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
+def test_gated_rmsnorm_matches_transformers_module(wdtype):
+    """core.py:390 applies transformers' Qwen3_5RMSNormGated to rows of head_v_dim (the module in the
+    model dtype, trtllm_stack.py:198): the restatement equals the module itself, bit for bit."""
+    Qwen3_5RMSNormGated = pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5").Qwen3_5RMSNormGated
+    g = gen(31)
+    hd, heads = 128, 4
+    x = (torch.randn(6, heads * hd, generator=g) * 2).to(torch.bfloat16)
+    z = (torch.randn(6, heads * hd, generator=g) * 2).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(hd, generator=g)).to(wdtype)
+    mod = Qwen3_5RMSNormGated(hd, eps=1e-6).to(dtype=wdtype)
+    with torch.no_grad():
+        mod.weight.copy_(w)
+        ref = mod(x.reshape(-1, hd), z.reshape(-1, hd)).reshape(x.shape)
+    assert torch.equal(R.gated_rmsnorm(x, z, w, 1e-6, hd), ref)
+    # known answers: z = 0 gates everything to 0; per-head (not per-row) normalization
+    assert torch.equal(R.gated_rmsnorm(x, torch.zeros_like(z), w, 1e-6, hd), torch.zeros_like(x))
+    scaled = x.clone()
+    scaled[:, :hd] *= 4  # head 0 scaled by a power of two: its normalized values, and only its, stay put
+    a, b = R.gated_rmsnorm(x, z, w, 1e-6, hd), R.gated_rmsnorm(scaled, z, w, 1e-6, hd)
+    assert torch.allclose(a.float(), b.float(), rtol=2 ** -7, atol=1e-6)
+    # heads of 2 hd (the same gain repeated) normalize over other groups: a wrong head split shows
+    assert not torch.equal(R.gated_rmsnorm(x, z, w, 1e-6, hd), R.gated_rmsnorm(x, z, torch.cat([w, w]), 1e-6, 2 * hd))
+
+
 def test_split_query_gate_takes_the_second_half_of_each_head():
     """core.py:231-232: q_proj rows viewed as [heads, 2 head_dim]; the gate is each head's second half."""
     heads, hd = 3, 8
