@@ -148,9 +148,23 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
 // then q(y) per token over the whole row. w has head_dim entries, shared by the
 // heads. head_dim divides 512 (64, 128, 256, 512): the 8-element pieces of one
 // head sit in head_dim / 8 consecutive lanes of one chunk, whose sum of squares
-// is an xor butterfly over those lanes (every lane of the group ends with the
-// same sum: each step adds the same two values). One wave per row.
+// is a butterfly over those lanes (group_sum). One wave per row.
 // ---------------------------------------------------------------------------
+// Sum over aligned groups of `group` lanes (8, 16, 32 or 64); every lane of a group ends with the same
+// value. Within 16-lane rows the partners come from DPP lane permutes (VALU ops): lane ^ 1, lane ^ 2,
+// then the mirror lane of the 8-lane half (the other quad) and of the 16-lane row (the other half).
+// Each level adds two values that every lane of the new group holds the same way round (addition
+// commutes), so the group stays uniform.
+__device__ __forceinline__ float group_sum(float v, int group) {
+  v = v + dpp_f32<0xB1, 0xf>(v);   // quad_perm [1, 0, 3, 2]
+  v = v + dpp_f32<0x4E, 0xf>(v);   // quad_perm [2, 3, 0, 1]
+  v = v + dpp_f32<0x141, 0xf>(v);  // row_half_mirror
+  if (group >= 16) v = v + dpp_f32<0x140, 0xf>(v);  // row_mirror
+  if (group >= 32) v = v + __shfl_xor(v, 16, 64);
+  if (group >= 64) v = v + __shfl_xor(v, 32, 64);
+  return v;
+}
+
 template <int MODE, int DT, int DTW, int NCH, bool FULL>
 __global__ __launch_bounds__(256) void gdn_norm_quant_vec(
     const void* __restrict__ x, int64_t ldx, const void* __restrict__ z, int64_t ldz, const void* __restrict__ w,
@@ -188,7 +202,7 @@ __global__ __launch_bounds__(256) void gdn_norm_quant_vec(
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) ss = dot2_sq<DT>(x_.w[c][i], ss);
-    for (int off = 1; off < group; off <<= 1) ss = ss + __shfl_xor(ss, off, 64);
+    ss = group_sum(ss, group);
     if (RC::valid(c, lane, K)) {
       const float var = ss / (float)head_dim;
       const float t = var + eps;
