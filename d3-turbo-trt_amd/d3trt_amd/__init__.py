@@ -3,7 +3,8 @@
 Public API mirrors d3trt/model/quant.py (``MODES``, ``fp8_supported``,
 ``resolve_mode``, ``quantizable``, ``quantize_weight``, ``quantize_rows``,
 ``QuantLinear``, ``make_linear``, ``summarize``) plus the fused MLP block
-(:class:`QuantMLP`) and the backbone projection stack (:class:`LinearStack`).
+(:class:`QuantMLP`), the backbone projection stack (:class:`LinearStack`) and
+pre-quantized weight files (:func:`save_quantized`, :func:`load_quantized`).
 The arithmetic lives in libd3w8a8.so (C ABI: include/d3w8a8.h); ``kernels``
 holds the thin torch wrappers over it.
 """
@@ -21,9 +22,11 @@ from .quant import (  # noqa: F401
 )
 from .mlp import QuantMLP  # noqa: F401
 from .stack import LinearStack  # noqa: F401
+from .weights import load_quantized, save_quantized  # noqa: F401
 from ._lib import LIB_PATH, LibraryMissing, version  # noqa: F401
 
 __all__ = [
     "MODES", "QuantLinear", "QuantMLP", "LinearStack", "fp8_supported", "make_linear", "quantizable", "quantize_rows",
-    "quantize_weight", "resolve_mode", "summarize", "LIB_PATH", "LibraryMissing", "version",
+    "quantize_weight", "resolve_mode", "summarize", "LIB_PATH", "LibraryMissing", "version", "save_quantized",
+    "load_quantized",
 ]
