@@ -144,7 +144,8 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
 // model dtype, trtllm_stack.py:198):
 //   h = x * rstd_head  (fp32; rstd = 1 / sqrt(mean over the head of x^2 + eps))
 //   h = w * DT(h)      (rounded to DT when w is DT; fp32 when w is fp32)
-//   y = DT( h * silu(z) ),  silu(z) = z / (1 + exp(-z)) in fp32
+//   y = DT( h * silu(z) ),  silu(z) = z / (1 + exp(-z)) in fp32 (hardware exp2 and
+//                            reciprocal: the kernel is VALU-bound)
 // then q(y) per token over the whole row. w has head_dim entries, shared by the
 // heads. head_dim divides 512 (64, 128, 256, 512): the 8-element pieces of one
 // head sit in head_dim / 8 consecutive lanes of one chunk, whose sum of squares
@@ -217,9 +218,11 @@ __global__ __launch_bounds__(256) void gdn_norm_quant_vec(
         h0 = wv[i] * h0;
         h1 = wv[i + 1] * h1;
         if constexpr (DTW == DT) round_pair_to<DT>(h0, h1);  // w (DT) * h (DT) is a DT tensor
-        const float e0 = expf(-zv[i]), e1 = expf(-zv[i + 1]);
+        // silu with the hardware exp2 and reciprocal (~1e-6 relative; only moves the final bf16
+        // rounding next to a rounding boundary)
+        const float e0 = __expf(-zv[i]), e1 = __expf(-zv[i + 1]);
         const float d0 = 1.0f + e0, d1 = 1.0f + e1;
-        const float s0 = zv[i] / d0, s1 = zv[i + 1] / d1;
+        const float s0 = zv[i] * __builtin_amdgcn_rcpf(d0), s1 = zv[i + 1] * __builtin_amdgcn_rcpf(d1);
         float p0 = h0 * s0, p1 = h1 * s1;
         y.put_pair(c, i / 2, p0, p1);
         amax = fmaxf(fmaxf(amax, fabsf(p0)), fabsf(p1));

@@ -37,6 +37,7 @@ def test_gdn_norm_quantize_matches_oracle(dev, mode, M, heads, hd):
     y = y.cpu()
     y_ref = R.gated_rmsnorm(x, z, w, 1e-6, hd)
     d = bf16_ulp_diff(y, y_ref)
+    print(f"1-ulp fraction {float((d > 0).float().mean()):.2e}")
     assert int(d.max()) <= 1 and float((d > 0).float().mean()) < 2e-3
     q_ref, s_ref = R.quantize_rows(y, mode)
     assert torch.equal(s.cpu(), s_ref)
