@@ -32,6 +32,9 @@
 //   swiglu  : weights interleaved in blocks of 32 rows [g0..g31, u0..u31, g32..];
 //             g = OUT(deq(gate)), u = OUT(deq(up)),
 //             h = OUT( OUT(g / (1 + exp(-g))) * u )                 (trtllm_stack.py:131-134)
+//             (exp and the reciprocal on the hardware exp2 / v_rcp_f32: ~1e-6
+//             relative, absorbed by the bf16 rounding of silu but next to a
+//             rounding boundary)
 //             and row_amax[m] = max(row_amax[m], |h|) by atomic max.
 //   residual: out = OUT( float(res[m, n]) + OUT(deq(acc)) )         (core.py:215)
 #pragma once
@@ -125,9 +128,7 @@ __device__ __forceinline__ void epilogue_edge(const GemmParams& p, ACC (&acc)[TM
             float uv = (float)acc[i][2 * jp + 1][r];
             uv = uv * st;
             uv = round_to<OUT>(uv * p.w_scale[cg + 32]);
-            const float e = expf(-gv);
-            const float den = 1.0f + e;
-            const float sl = round_to<OUT>(gv / den);
+            const float sl = round_to<OUT>(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)));
             const float h = round_to<OUT>(sl * uv);
             store_elem<OUT>(p.out, orow * p.ldo + (cg >> 6) * 32 + (cg & 31), h);
             rmax = fmaxf(rmax, fabsf(h));
@@ -251,9 +252,7 @@ __device__ __forceinline__ void epilogue_lds(const GemmParams& p, ACC (&acc)[TM]
             float uv = (float)acc[i][2 * jp + 1][4 * g + c];
             uv = uv * st[i];
             uv = round_to<OUT>(uv * sc[2 * jp + 1][g][c]);
-            const float e = expf(-gv);
-            const float den = 1.0f + e;
-            const float sl = round_to<OUT>(gv / den);
+            const float sl = round_to<OUT>(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)));
             h[c] = round_to<OUT>(sl * uv);
             rmax = fmaxf(rmax, fabsf(h[c]));
           }
