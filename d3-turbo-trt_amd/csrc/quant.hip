@@ -15,6 +15,7 @@
 
 #include <stdlib.h>
 
+#include <atomic>
 #include <mutex>
 #include <utility>
 #include <vector>
@@ -43,15 +44,15 @@ int row_blocks_per_cu() {
 }
 
 int device_cu_count() {
-  static int cus[64] = {0};
+  static std::atomic<int> cus[64];  // 0 until queried; concurrent first calls store the same value
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cus[dev] == 0) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 // ---------------------------------------------------------------------------
