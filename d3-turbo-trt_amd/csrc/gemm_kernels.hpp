@@ -680,8 +680,9 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   constexpr int FW = MODE == kInt8 ? 1 : 2;     // 16-byte LDS words per MFMA operand
   constexpr int NMF = SUB * TM * TN;            // MFMAs per step
   // MFMAs issued before the barrier (cover the waves' skew at it); 4 for the three-column-block tiles
-  // (256x192: QKV 107.7 -> 101.1 us at M = 4096, same box), 2 elsewhere (256x256 unchanged by 4)
-  constexpr int PRE = TN == 3 ? 4 : (NMF >= 4 ? 2 : 1);
+  // (256x192: QKV 107.7 -> 101.1 us at M = 4096, same box) and the FP8 128-byte-step tile (M = 128
+  // question GEMMs: 1-3%), 2 elsewhere (256x256 unchanged by 4)
+  constexpr int PRE = (TN == 3 || (BK == 128 && MODE == kFp8)) ? 4 : (NMF >= 4 ? 2 : 1);
   constexpr int SLOTS = NMF - PRE;
   constexpr int NBW = SUB * TN * FW;            // B words read per step
   static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "DMA split");
