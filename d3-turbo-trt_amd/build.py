@@ -6,6 +6,8 @@ results:
   -ffp-contract=off      no a*b+c fusion (the eager torch chain rounds twice)
   (default) correctly rounded fp32 division / sqrt
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed-fp32 VALU ops
+  -Werror=inline-asm     inline asm the compiler cannot honour (a reserved register in a
+                         clobber list) fails the build
 """
 
 from __future__ import annotations
@@ -30,6 +32,7 @@ FLAGS = [
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
+    "-Werror=inline-asm",  # e.g. a reserved register (m0) in a clobber list, which the compiler ignores
 ]
 
 

@@ -96,15 +96,35 @@ __device__ __forceinline__ float round_to(float v) {
 // zero in int8 and FP8 once the sign of x is put back on q'. Three VALU ops
 // per element replace a correctly rounded fp32 division (~10 ops); the
 // exhaustive CPU check of this identity is tests/c/fma_division.c.
+//
+// Non-finite scales (a row holding an inf or a NaN) keep torch's quotients:
+// scale NaN gives r = NaN and a NaN quotient; scale inf gives r = 0, and the
+// correction runs with c = 0 (e = x, q' = q = x * 0), so a finite x yields a
+// zero of x's sign and an infinite x a NaN, as x / inf does. With c = scale,
+// q * inf would turn every finite element's residual into a NaN.
 struct RowScale {
-  float s;
-  float r;
+  float s;  // the scale (stored per token)
+  float r;  // RN(1 / s)
+  float c;  // s, or 0 when s is infinite (the correction step's multiplier)
 };
-__device__ __forceinline__ RowScale make_row_scale(float s) { return RowScale{s, 1.0f / s}; }
+__device__ __forceinline__ RowScale make_row_scale(float s) {
+  return RowScale{s, 1.0f / s, __builtin_isinf(s) ? 0.0f : s};
+}
 __device__ __forceinline__ float div_row(float x, const RowScale& r) {
   const float q = x * r.r;
-  const float e = __builtin_fmaf(-q, r.s, x);
+  const float e = __builtin_fmaf(-q, r.c, x);
   return __builtin_fmaf(e, r.r, q);
+}
+
+// Running max of magnitudes that keeps a NaN, as torch's x.abs().amax() does:
+// the bit patterns of values >= 0 order like the values as unsigned integers,
+// and |NaN| (sign cleared) lies above +inf. m is a previous result (>= 0 or NaN).
+__device__ __forceinline__ float amax_acc(float m, float v) {
+  return __uint_as_float(max(__float_as_uint(m), __float_as_uint(fabsf(v))));
+}
+// max of two such results
+__device__ __forceinline__ float amax_join(float a, float b) {
+  return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
 }
 
 // int8: clamp(rint(x / scale), -127, 127) (quant.py:86, 100). Adding 1.5 * 2^23
@@ -129,20 +149,30 @@ __device__ __forceinline__ uint32_t quant_i8_bits(float x, const RowScale& r) {
 // fp8: e4m3fn_rne(clamp(x / scale, -448, 448))   (quant.py:83, 98); the
 // hardware converter rounds to nearest even and is OCP E4M3 on gfx950. The
 // quotient carries the sign of x also when it is zero (-0 encodes as 0x80).
+// CLAMP as for int8: with the scale from the row's own amax, |x / scale| <=
+// 448 (1 + 2^-23), which rounds to 448 (the next E4M3 step would be 480, so
+// everything below 464 rounds down), and a NaN quotient reaches the converter
+// as a NaN (fminf / fmaxf would turn it into +-448).
 __device__ __forceinline__ float div_row_signed(float x, const RowScale& r) {
   const float q = div_row(x, r);
   return __uint_as_float((__float_as_uint(q) & 0x7fffffffu) | (__float_as_uint(x) & 0x80000000u));
 }
+template <bool CLAMP>
+__device__ __forceinline__ float f8_quotient(float x, const RowScale& r) {
+  const float v = div_row_signed(x, r);
+  return CLAMP ? fminf(fmaxf(v, -kFp8Max), kFp8Max) : v;
+}
+template <bool CLAMP = false>
 __device__ __forceinline__ uint32_t quant_f8_pair(float x0, float x1, const RowScale& r) {
-  float a = fminf(fmaxf(div_row_signed(x0, r), -kFp8Max), kFp8Max);
-  float b = fminf(fmaxf(div_row_signed(x1, r), -kFp8Max), kFp8Max);
+  const float a = f8_quotient<CLAMP>(x0, r), b = f8_quotient<CLAMP>(x1, r);
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
 }
 // four values -> four E4M3 bytes of one word (the second conversion writes the high half)
+template <bool CLAMP = false>
 __device__ __forceinline__ uint32_t quant_f8_quad(const float* x, const RowScale& r) {
   float v[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = fminf(fmaxf(div_row_signed(x[i], r), -kFp8Max), kFp8Max);
+  for (int i = 0; i < 4; ++i) v[i] = f8_quotient<CLAMP>(x[i], r);
   const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], lo, true);
 }
@@ -173,9 +203,9 @@ __device__ __forceinline__ float wave_reduce(float v, OP op) {
   v = op(v, dpp_f32<0x143, 0xc>(v));  // row_bcast:31 into rows 2 and 3
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
-// max over the wave of values >= 0 (absolute values)
+// max over the wave of magnitudes (values >= 0, or NaN, which wins: amax_join)
 __device__ __forceinline__ float wave_max(float v) {
-  return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
+  return wave_reduce(v, [](float a, float b) { return amax_join(a, b); });
 }
 // sum over the wave, in the fixed order of the DPP steps above
 __device__ __forceinline__ float wave_sum(float v) {

@@ -80,7 +80,6 @@ TileShape shape_of(int tile) {
   return {0, 0, false, 0};
 }
 
-constexpr int kCUs = 256;              // MI355X compute units
 constexpr int kMinSplitBytes = 1024;   // bytes of K per split at least
 
 // The DMA kernels address operands as a tile base plus a 32-bit per-lane offset.
@@ -90,7 +89,7 @@ bool dma_offsets_fit(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) 
 }
 
 // Rounds of tiles the chip runs one after the other (one workgroup per CU).
-int64_t rounds(int64_t tiles) { return (tiles + kCUs - 1) / kCUs; }
+int64_t rounds(int64_t tiles, int64_t cus) { return (tiles + cus - 1) / cus; }
 
 // Tile choice (measured on MI355X): with K % 64 == 0, the 4-wave 256x256 DMA
 // tile once there are enough such tiles to cover the chip, 256x128 for
@@ -102,33 +101,34 @@ int64_t rounds(int64_t tiles) { return (tiles + kCUs - 1) / kCUs; }
 // epilogues without gate/up pairs). Measured: 1440 x 6144 x 4096 INT8 70.0 ->
 // 60.6 us; 1280 rows keep 256x128 (44.2 us, 256x192 52.5 us), as the rule says. M <= 128 (a
 // 256-row tile would compute half its rows for nothing) streams the weights:
-// 128x128 with 128-byte K steps when K allows.
-int choose_tile(int64_t M, int64_t N, int64_t K, bool fit, int epi) {
+// 128x128 with 128-byte K steps when K allows. Tile counts are weighed against
+// the device's compute units (`cus`; the thresholds were measured on 256).
+int choose_tile(int64_t M, int64_t N, int64_t K, bool fit, int epi, int64_t cus) {
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
   if (K % 64 == 0 && fit) {
     if (M <= 128) return K % 128 == 0 ? kDma128w4k128 : kDma128w4;
-    if (t256 >= 192) {
+    if (4 * t256 >= 3 * cus) {  // 192 tiles on 256 CUs
       if (epi != kEpiSwiGLU && N % 192 == 0) {
         const int64_t t192 = ((M + 255) / 256) * (N / 192);
-        if (rounds(t192) * 192 * 10 <= rounds(t256) * 256 * 9) return kDma256x192w4;
+        if (rounds(t192, cus) * 192 * 10 <= rounds(t256, cus) * 256 * 9) return kDma256x192w4;
       }
       return kDma256w4;
     }
-    if (t256x128 >= 160) {
+    if (8 * t256x128 >= 5 * cus) {  // 160 tiles on 256 CUs
       // the same round count rule against 256x128 (ragged question batches: 1440 rows x N = 6144 is
       // 288 tiles of 256x128, one round and 32 tiles, but 192 tiles of 256x192, one round)
       if (epi != kEpiSwiGLU && N % 192 == 0) {
         const int64_t t192 = ((M + 255) / 256) * (N / 192);
-        if (rounds(t192) * 192 * 10 <= rounds(t256x128) * 128 * 9) return kDma256x192w4;
+        if (rounds(t192, cus) * 192 * 10 <= rounds(t256x128, cus) * 128 * 9) return kDma256x192w4;
       }
       return kDma256x128w4;
     }
     return kDma128w4;
   }
-  if (t256 >= 256) return kTile256;
-  if (t128 >= 192) return kTile128;
+  if (t256 >= cus) return kTile256;
+  if (4 * t128 >= 3 * cus) return kTile128;
   return kTile64x128;
 }
 
@@ -136,8 +136,8 @@ int choose_tile(int64_t M, int64_t N, int64_t K, bool fit, int epi) {
 // each split at least kMinSplitBytes of K. Measured on MI355X at M = 128
 // (weights streamed from HBM): more splits cost more in partial sums and the
 // reduce launch than the extra workgroups gain.
-int choose_ksplit(int64_t tiles, int nk, int bk) {
-  const int64_t target = kCUs;
+int choose_ksplit(int64_t tiles, int nk, int bk, int64_t cus) {
+  const int64_t target = cus;
   if (2 * tiles > target) return 1;
   int64_t s = (target + tiles - 1) / tiles;
   s = std::min<int64_t>(s, nk / (kMinSplitBytes / bk));
@@ -152,7 +152,8 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, in
   GemmPlan pl{};
   pl.ksplit = 1;
   const bool fit = dma_offsets_fit(M, N, K, lda, ldw);
-  pl.tile = tile < 0 ? choose_tile(M, N, K, fit, epi) : tile;
+  const int64_t cus = device_cu_count();
+  pl.tile = tile < 0 ? choose_tile(M, N, K, fit, epi, cus) : tile;
   if (pl.tile >= kTileCount) return pl.error = "unknown tile", pl;
   if (pl.tile == kDma256x192w4 && epi == kEpiSwiGLU)
     return pl.error = "the 256x192 tile has 3 column blocks per wave; SwiGLU needs gate/up pairs", pl;
@@ -175,7 +176,7 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, in
     pl.ksplit = ksplit;
   } else if (sh.dma && sh.bm == 128 && sh.bn == 128 && tiles > 0 && ws_bytes > 0) {
     const int64_t room = ws_bytes / (tiles * slot);
-    const int s = (int)std::min<int64_t>(choose_ksplit(tiles, nk, sh.bk), room);
+    const int s = (int)std::min<int64_t>(choose_ksplit(tiles, nk, sh.bk, cus), room);
     pl.ksplit = s >= 2 ? s : 1;
   }
   pl.ws_bytes = pl.ksplit > 1 ? tiles * pl.ksplit * slot : 0;

@@ -131,11 +131,11 @@ __device__ __forceinline__ void epilogue_edge(const GemmParams& p, ACC (&acc)[TM
             const float sl = round_to<OUT>(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)));
             const float h = round_to<OUT>(sl * uv);
             store_elem<OUT>(p.out, orow * p.ldo + (cg >> 6) * 32 + (cg & 31), h);
-            rmax = fmaxf(rmax, fabsf(h));
+            rmax = amax_acc(rmax, h);
           }
         }
       if (p.row_amax) {
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+        rmax = amax_join(rmax, __shfl_xor(rmax, 32, 64));
         if (lhalf == 0 && rok) atomicMax((unsigned int*)(p.row_amax + row), __float_as_uint(rmax));
       }
     } else {
@@ -254,13 +254,13 @@ __device__ __forceinline__ void epilogue_lds(const GemmParams& p, ACC (&acc)[TM]
             uv = round_to<OUT>(uv * sc[2 * jp + 1][g][c]);
             const float sl = round_to<OUT>(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)));
             h[c] = round_to<OUT>(sl * uv);
-            rmax = fmaxf(rmax, fabsf(h[c]));
+            rmax = amax_acc(rmax, h[c]);
           }
           lds_put4<OUT, E::ES>(stage + E::at(lrow, (jp * 32 + g * 8 + lhalf * 4) * E::ES), h);
           if (g == 3) __builtin_amdgcn_sched_barrier(0);
         }
       if (p.row_amax) {
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));  // lanes l and l + 32 share the row
+        rmax = amax_join(rmax, __shfl_xor(rmax, 32, 64));  // lanes l and l + 32 share the row
         if (lhalf == 0) atomicMax((unsigned int*)(p.row_amax + wrow0 + i * 32 + lrow), __float_as_uint(rmax));
       }
     } else {
@@ -547,8 +547,9 @@ __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F
 // at LDS lds_base + OFF + 16 l. Issued as inline asm so the compiler does not
 // model the LDS write (it would otherwise insert vmcnt(0) before LDS reads it
 // cannot prove disjoint, draining the pipeline); every wait on this DMA is
-// explicit (wait_vmcnt + barrier). M0 holds the LDS address; the s_nop covers
-// the M0-write -> LDS-DMA hazard.
+// explicit (wait_vmcnt + barrier). M0 holds the LDS address: it is an input
+// operand bound to m0 ("{m0}"), so the compiler writes m0 itself and knows
+// its value at every point; the s_nop covers the M0-write -> LDS-DMA hazard.
 // A wave-uniform pointer, pinned to SGPRs (the DMA asm takes it as an SGPR pair).
 __device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* q) {
   const uint64_t v = (uint64_t)(uintptr_t)q;
@@ -560,12 +561,11 @@ __device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* q) {
 template <int OFF>
 __device__ __forceinline__ void dma16(const uint8_t* gbase, uint32_t voff, uint32_t lds_base) {
   asm volatile(
-      "s_add_u32 m0, %1, %2\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, %3"
+      "global_load_lds_dwordx4 %0, %1"
       :
-      : "v"(voff), "s"(lds_base), "i"(OFF), "s"(gbase)
-      : "memory", "m0", "scc");
+      : "v"(voff), "s"(gbase), "{m0}"(lds_base + (uint32_t)OFF)
+      : "memory");
 }
 
 // Split-K, first half: every workgroup of a tile stores its raw accumulators

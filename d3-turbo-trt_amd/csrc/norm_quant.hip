@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
               p0 = p0 * g[i];
               p1 = p1 * g[i + 1];
               y.put_pair(c, i / 2, p0, p1);
-              amax = fmaxf(fmaxf(amax, fabsf(p0)), fabsf(p1));
+              amax = amax_acc(amax_acc(amax, p0), p1);
             }
           }
         }
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(256) void gdn_norm_quant_vec(
         const float s0 = zv[i] * __builtin_amdgcn_rcpf(d0), s1 = zv[i + 1] * __builtin_amdgcn_rcpf(d1);
         float p0 = h0 * s0, p1 = h1 * s1;
         y.put_pair(c, i / 2, p0, p1);
-        amax = fmaxf(fmaxf(amax, fabsf(p0)), fabsf(p1));
+        amax = amax_acc(amax_acc(amax, p0), p1);
       }
     }
   }

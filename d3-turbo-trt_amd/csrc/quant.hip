@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void quant_rows_generic(const void* __restrict
   if (row >= M) return;
   const int64_t base = row * ldx;
   float amax = 0.0f;
-  for (int64_t k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(load_elem<DT>(x, base + k)));
+  for (int64_t k = lane; k < K; k += 64) amax = amax_acc(amax, load_elem<DT>(x, base + k));
   amax = wave_max(amax);
   const RowScale s = scale_from_amax<MODE>(amax);
   uint8_t* qr = (uint8_t*)q + row * ldq;
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256) void gate_quant_vec(const void* __restrict__ x
         round_pair_to<DT>(s0, s1);  // torch.sigmoid's output in the tensor dtype
         float p0 = v[i] * s0, p1 = v[i + 1] * s1;
         y.put_pair(c, i / 2, p0, p1);
-        amax = fmaxf(fmaxf(amax, fabsf(p0)), fabsf(p1));
+        amax = amax_acc(amax_acc(amax, p0), p1);
       }
     }
   }

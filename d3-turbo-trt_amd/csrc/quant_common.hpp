@@ -123,7 +123,7 @@ struct RowChunks {
         float v[8];
         get(c, v);
 #pragma unroll
-        for (int i = 0; i < 8; i += 2) m = fmaxf(fmaxf(m, fabsf(v[i])), fabsf(v[i + 1]));
+        for (int i = 0; i < 8; i += 2) m = amax_acc(amax_acc(m, v[i]), v[i + 1]);
       }
     }
     return m;
@@ -187,16 +187,17 @@ __device__ __forceinline__ void quant_store8(void* q, const float* v, const RowS
     lo = pack_low_bytes(b[0], b[1], b[2], b[3]);
     hi = pack_low_bytes(b[4], b[5], b[6], b[7]);
   } else {
-    lo = quant_f8_quad(v, r);
-    hi = quant_f8_quad(v + 4, r);
+    lo = quant_f8_quad<CLAMP>(v, r);
+    hi = quant_f8_quad<CLAMP>(v + 4, r);
   }
   *(uint2*)q = make_uint2(lo, hi);
 }
 
-// scale = max(amax, 1e-12) / (127 | 448)   (quant.py:95-99: clamp_min, then an fp32 division)
+// scale = max(amax, 1e-12) / (127 | 448)   (quant.py:95-99: clamp_min, then an fp32 division);
+// a NaN amax stays NaN, as torch's clamp_min keeps it (fmaxf would return the floor)
 template <int MODE>
 __device__ __forceinline__ RowScale scale_from_amax(float amax) {
-  amax = fmaxf(amax, kAmaxFloor);
+  amax = amax < kAmaxFloor ? kAmaxFloor : amax;
   return make_row_scale(amax / (MODE == kInt8 ? kInt8Max : kFp8Max));
 }
 

@@ -7,6 +7,7 @@ stream. There is no CPU implementation behind any of them.
 from __future__ import annotations
 
 import ctypes
+import threading
 from typing import Optional, Sequence
 
 import torch
@@ -186,6 +187,14 @@ def quantize_rows_ragged(x: torch.Tensor, lengths: Sequence[int], mode: str, *,
         raise ValueError(f"at most {_lib.MAX_SEGMENTS} blocks per ragged batch, got {B}")
     x2 = x.reshape(B * W, K)
     x2 = _rows(x2, "x")
+    if out is not None:
+        # the kernel zeroes every padded row b * W + t of `out` (t >= lengths[b]) through its row pitch
+        _gpu(out, "out")
+        if out.dim() != 2 or out.stride(1) != 1 or out.shape[0] < B * W or out.stride(0) < out.shape[1]:
+            raise ValueError(f"out must be a row-major [>= {B * W}, N] tensor, got shape {tuple(out.shape)} "
+                             f"stride {tuple(out.stride())}")
+        if out.dtype not in _DT:
+            raise ValueError(f"unsupported out dtype {out.dtype}")
     T = sum(lengths)
     dev = x.device
     host_lengths = (ctypes.c_int32 * max(B, 1))(*lengths)
@@ -202,7 +211,9 @@ def quantize_rows_ragged(x: torch.Tensor, lengths: Sequence[int], mode: str, *,
         dtype_code(out.dtype) if out is not None else 0, out.stride(0) if out is not None else 0, N,
         _stream(x2))
     _lib.check(rc, "quantize_rows_ragged")
-    return q[:T], s[:T], row_map[:T]
+    row_map = row_map[:T]
+    row_map.d3_rows = B * W  # output rows the map addresses; gemm() checks its `out` against it
+    return q[:T], s[:T], row_map
 
 
 def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.Tensor,
@@ -252,8 +263,13 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
                                  or not row_amax.is_contiguous()):
         raise ValueError("row_amax must be a contiguous float32 buffer with one entry per GEMM row")
     if row_map is not None:
-        if row_map.dtype != torch.int32 or row_map.numel() != M:
-            raise ValueError("row_map must be int32 with one entry per GEMM row")
+        if row_map.dtype != torch.int32 or row_map.numel() != M or not row_map.is_contiguous():
+            raise ValueError("row_map must be contiguous int32 with one entry per GEMM row")
+        # rows a map from quantize_rows_ragged can address (its batch's B * W); a map built elsewhere
+        # must hold indices below out.shape[0] (checking its values here would synchronize the device)
+        need = getattr(row_map, "d3_rows", M)
+        if out.shape[0] < need:
+            raise ValueError(f"output tensor has {out.shape[0]} rows; the row_map addresses {need}")
     for t, name in ((a_scale, "a_scale"), (w_scale, "w_scale")):
         if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
             raise ValueError(f"{name} must be contiguous float32")
@@ -262,7 +278,14 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
             raise ValueError("dequantizing epilogues need a_scale [M] and w_scale [N]")
     lib = _lib.load()
     st = _stream(a)
-    ws = workspace(a.device, st) if ksplit != 1 else None
+    ws = None
+    if ksplit != 1:
+        # only a plan that splits K touches the workspace (the state-pass shapes never do)
+        need = lib.d3w8a8_gemm_workspace(M, N, K, a.stride(0), w.stride(0), tile, ksplit, WORKSPACE_BYTES)
+        if need < 0:
+            _lib.check(_lib.EINVAL, "gemm")
+        if need > 0:
+            ws = workspace(a.device, st)
     rc = lib.d3w8a8_gemm_ws(
         mode_code(mode), a.data_ptr(), a.stride(0), _ptr(a_scale), w.data_ptr(), w.stride(0), _ptr(w_scale),
         M, N, K, epilogue, dtype_code(odt) if epilogue != _lib.EPI_RAW else 0, out.data_ptr(), out.stride(0),
@@ -274,24 +297,29 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
 
 WORKSPACE_BYTES = 64 << 20
 _workspaces: dict = {}
+_workspaces_lock = threading.Lock()
 
 
 def workspace(device: torch.device, stream: int) -> torch.Tensor:
     """The split-K workspace of one (device, stream): WORKSPACE_BYTES of device memory.
 
-    GEMMs on one stream run in order, so they can share it. The first GEMM on
-    a stream must not be inside a graph capture (the allocation would be
-    captured); warm the stream up eagerly.
+    GEMMs on one stream run in order, so they can share it; streams never
+    share one. The first split-K GEMM on a stream allocates it through torch's
+    caching allocator. Inside a graph capture (torch.cuda.graph captures on a
+    stream of its own) that allocation comes from the graph's private memory
+    pool, which torch allows; the buffer stays cached for the capture stream,
+    so later captures on it reuse the same memory. Graphs captured on one
+    stream therefore share a workspace: replay them in order (one stream).
     """
     device = torch.device(device)
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _workspaces.get(key)
     if ws is None:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("the first GEMM on a stream runs eagerly (it allocates the split-K workspace); "
-                               "warm the stream up before capturing a graph on it")
-        ws = torch.empty(WORKSPACE_BYTES, dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
+        with _workspaces_lock:
+            ws = _workspaces.get(key)
+            if ws is None:
+                ws = torch.empty(WORKSPACE_BYTES, dtype=torch.uint8, device=device)
+                _workspaces[key] = ws
     return ws
 
 

@@ -159,7 +159,8 @@ class GraphedStack:
 
     def __init__(self, stack: LinearStack, rows: int):
         dev = next(stack.buffers()).device
-        self.static_in = torch.zeros(rows, stack.hidden, dtype=torch.bfloat16, device=dev)
+        dtype = stack.layers[0].input_layernorm.dtype  # the stack's activation dtype (its norm weights')
+        self.static_in = torch.zeros(rows, stack.hidden, dtype=dtype, device=dev)
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):

@@ -86,6 +86,76 @@ def test_quantize_rows_amax_bit_exact(dev, mode, M, Kd):
 
 
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
+def test_quantize_rows_amax_external_amax_clamps(dev, mode):
+    """An amax from outside that is not the row's own max: above it the codes shrink, below it the
+    quotients pass the code range and clamp (the path the row's own amax never takes)."""
+    g = gen(77)
+    M, Kd = 12, 4096
+    h = R.outlier_activations(g, M, Kd)
+    own = h.float().abs().amax(dim=1)
+    amax = own * torch.tensor([2.0, 0.5, 1.0, 0.25] * 3)
+    q_ref, s_ref = R.quantize_rows_with_amax(h, amax, mode)
+    q, s = K.quantize_rows_amax(h.to(dev), amax.to(dev), mode)
+    assert torch.equal(s.cpu(), s_ref)
+    assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8))
+
+
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
+def test_fp8_int8_quotient_just_above_the_code_range(dev, mode):
+    """Rows whose max element divided by the fp32 scale lands just above 127 / 448 in fp32 (the
+    reference clamps it; the kernels, which skip the clamp for the row's own amax, must round it to
+    127 / 448 as well)."""
+    lim = 127.0 if mode == "int8" else 448.0
+    cand = torch.linspace(0.5, 64.0, 200001, dtype=torch.float32)
+    over = cand[(cand / (cand / lim)) > lim][:64]
+    assert over.numel() == 64
+    x = torch.randn(64, 1024, generator=gen(5)) * 0.1
+    x[:, 17] = over
+    x[:, 900] = -over
+    q_ref, s_ref = R.quantize_rows(x, mode)
+    q, s = K.quantize_rows(x.to(dev), mode)
+    assert torch.equal(s.cpu(), s_ref)
+    assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8))
+
+
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
+def test_non_finite_rows_keep_nan_scale(dev, mode):
+    """A NaN in a row makes the reference's amax, scale and linear output NaN (x.abs().amax() and
+    clamp_min keep NaN, quant.py:95-100); an inf gives an inf scale and zero codes for the finite
+    elements (x / inf). Finite rows around them stay bit-exact."""
+    g = gen(31)
+    M, Kd, N = 8, 1024, 256
+    x = R.outlier_activations(g, M, Kd).float()
+    x[1, 5] = float("nan")
+    x[3, 700] = float("inf")
+    x[4, 2] = -float("inf")
+    x[6, 1000] = float("nan")
+    x[6, 3] = float("inf")
+    bad = [1, 3, 4, 6]
+    good = [r for r in range(M) if r not in bad]
+    for dtype in (torch.float32, torch.bfloat16):
+        xd = x.to(dtype)
+        q_ref, s_ref = R.quantize_rows(xd, mode)
+        q, s = K.quantize_rows(xd.to(dev), mode)
+        torch.testing.assert_close(s.cpu(), s_ref, rtol=0, atol=0, equal_nan=True)
+        assert torch.isnan(s.cpu()[[1, 6]]).all() and torch.isinf(s.cpu()[[3, 4]]).all()
+        assert torch.equal(q.cpu()[good].view(torch.uint8), q_ref[good].view(torch.uint8))
+        # finite elements of the inf rows: x / inf is a zero of x's sign
+        fin = torch.isfinite(xd[[3, 4]])
+        assert torch.all(q.cpu()[[3, 4]].float()[fin] == 0)
+    # the whole linear: NaN rows come out NaN, finite rows bit-exact (int8) / within the fp8 bar
+    wq, ws = R.quantize_weight(R.gaussian_weight(g, N, Kd), mode)
+    xb = x.to(torch.bfloat16)
+    ref = R.emulated_linear(xb, wq, ws, mode, torch.bfloat16)
+    q, s = K.quantize_rows(xb.to(dev), mode)
+    out = K.gemm(mode, q, s.view(-1), wq.to(dev), ws.to(dev)).cpu()
+    assert torch.isnan(out[[1, 6]]).all() and torch.isnan(ref[[1, 6]]).all()
+    assert not torch.isfinite(out[[3, 4]]).any()
+    if mode == "int8":
+        assert torch.equal(out[good], R.linear_forward(xb[good], wq, ws, "int8", torch.bfloat16))
+
+
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
 @pytest.mark.parametrize("zero_centered", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,Kd", [(64, 4096), (33, 1024), (8, 12288)])

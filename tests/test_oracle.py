@@ -71,6 +71,46 @@ def test_int8_quant_is_nearest_integer_bruteforce():
             assert int(q[r, c]) == int(want)
 
 
+# ---------------------------------------------------------------- quantize_rows_with_amax
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
+def test_with_amax_equals_quantize_rows_at_the_row_max(mode):
+    # given the row's own max |x| it is quantize_rows (pinned above) bit for bit; a dropped floor,
+    # a swapped 127 / 448 or a missing division differs on these rows
+    g = gen(3)
+    x = R.outlier_activations(g, 24, 520).float()
+    x[3] = 0.0  # the 1e-12 floor
+    x[5, 7] = 1e-30  # a denormal-free tiny row amax
+    x[5, :7] = 0.0
+    x[5, 8:] = 0.0
+    q_ref, s_ref = R.quantize_rows(x, mode)
+    q, s = R.quantize_rows_with_amax(x, x.abs().amax(dim=1), mode)
+    assert torch.equal(s, s_ref)
+    assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
+
+
+def test_with_amax_known_answers_and_clamp():
+    # amax above the row max: scale amax / 127 = 1 exactly, so q = round_half_even(x)
+    x = torch.tensor([[1.0, -0.5, 2.5, 3.5], [100.0, 3.0, -100.0, 0.0]])
+    q, s = R.quantize_rows_with_amax(x[:1], torch.tensor([127.0]), "int8")
+    assert float(s) == 1.0 and q.tolist() == [[1, 0, 2, 4]]
+    # amax below the row max: quotients beyond 127 clamp symmetrically (never -128)
+    q, s = R.quantize_rows_with_amax(x[1:], torch.tensor([50.0]), "int8")
+    assert float(s) == np.float32(50.0) / np.float32(127.0)
+    quot = (x[1:] / s).tolist()[0]
+    assert q.tolist() == [[127, round(quot[1]), -127, 0]]
+    # fp8: scale amax / 448, quotient clamped to +-448 before the cast
+    q, s = R.quantize_rows_with_amax(torch.tensor([[1000.0, -1000.0, 2.0]]), torch.tensor([448.0]), "fp8")
+    assert float(s) == 1.0 and q.float().tolist() == [[448.0, -448.0, 2.0]]
+
+
+def test_with_amax_keeps_a_nan_amax():
+    # torch's clamp_min keeps NaN: a NaN row amax gives a NaN scale, as quantize_rows gives for a NaN row
+    x = torch.tensor([[1.0, float("nan"), 2.0]])
+    _, s_ref = R.quantize_rows(x, "int8")
+    _, s = R.quantize_rows_with_amax(x, torch.tensor([float("nan")]), "int8")
+    assert torch.isnan(s_ref).all() and torch.isnan(s).all()
+
+
 # ---------------------------------------------------------------- FP8 (OCP E4M3)
 def test_torch_e4m3fn_cast_matches_spec_encoder():
     # every finite code, every midpoint, neighbours of both, and a dense sweep of fp32 bit patterns
