@@ -98,22 +98,26 @@ class LinearStack(nn.Module):
         lengths = [int(n) for n in lengths]
         if len(lengths) != B or any(n < 0 or n > W for n in lengths):
             raise ValueError(f"lengths {lengths} do not fit a [{B}, {W}] batch")
-        rows = self._packed_rows(tuple(lengths), W, x.device)
+        rows, pad = self._packed_rows(tuple(lengths), W, x.device)
         flat = x.reshape(B * W, H)
-        out = torch.zeros_like(flat)
+        out = torch.empty_like(flat, memory_format=torch.contiguous_format)
         if rows.numel():
             packed = flat.index_select(0, rows)
             res = self.graphed(rows.numel())(packed) if graph else self.forward(packed)
             out.index_copy_(0, rows, res)
+        if pad.numel():
+            out.index_fill_(0, pad, 0)  # only the padded rows: no pass over the whole batch
         return out.reshape(B, W, H)
 
-    def _packed_rows(self, lengths: tuple, width: int, device) -> torch.Tensor:
-        """Device indices of the valid rows of a [B, width] batch (cached per shape)."""
+    def _packed_rows(self, lengths: tuple, width: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+        """Device indices of the valid rows and of the padded rows of a [B, width] batch (cached per
+        shape)."""
         cache = self.__dict__.setdefault("_rows_cache", {})
         key = (lengths, width, str(device))
         if key not in cache:
             idx = [b * width + t for b, n in enumerate(lengths) for t in range(n)]
-            cache[key] = torch.tensor(idx, dtype=torch.long).to(device)
+            pad = [b * width + t for b, n in enumerate(lengths) for t in range(n, width)]
+            cache[key] = (torch.tensor(idx, dtype=torch.long).to(device), torch.tensor(pad, dtype=torch.long).to(device))
         return cache[key]
 
     def graphed(self, rows: int) -> "GraphedStack":
@@ -161,7 +165,9 @@ class GraphedStack:
         dev = next(stack.buffers()).device
         dtype = stack.layers[0].input_layernorm.dtype  # the stack's activation dtype (its norm weights')
         self.static_in = torch.zeros(rows, stack.hidden, dtype=dtype, device=dev)
-        side = torch.cuda.Stream(device=dev)
+        # one capture stream per stack: its graphs share that stream's split-K workspace (replays run in
+        # order on the caller's stream) instead of each capture bringing its own
+        side = stack.__dict__.setdefault("_capture_stream", torch.cuda.Stream(device=dev))
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
             for _ in range(2):  # warm the allocator (and the stream's split-K workspace) outside the capture

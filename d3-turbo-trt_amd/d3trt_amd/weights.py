@@ -9,9 +9,9 @@ Loading copies them back, with no re-quantization. A QuantMLP's gate_up weight i
 the row order its fused SwiGLU epilogue reads (blocks of 32 gate rows, then 32 up rows),
 which the metadata records.
 
-File layout: tensors ``<name>.weight`` / ``<name>.weight_scale`` for a linear, and
-``<name>.gate_up_proj.*`` / ``<name>.down_proj.*`` for an MLP; the metadata holds
-``format`` and one JSON entry per module name.
+File layout: tensors ``<name>.weight`` / ``<name>.weight_scale`` for a linear,
+``<name>.gate_up_proj.*`` / ``<name>.down_proj.*`` for an MLP, and ``<name>`` for a plain
+tensor stored as it is (a norm gain); the metadata holds ``format`` and one JSON entry per name.
 """
 
 from __future__ import annotations
@@ -36,8 +36,9 @@ def _linear_tensors(prefix: str, lin: QuantLinear, out: dict) -> None:
     out[f"{prefix}.weight_scale"] = lin.weight_scale.detach().contiguous().cpu()
 
 
-def save_quantized(path: str, modules: Mapping[str, nn.Module]) -> None:
-    """Write the quantized buffers of ``modules`` (name -> QuantLinear or QuantMLP) to ``path``."""
+def save_quantized(path: str, modules: Mapping[str, nn.Module | torch.Tensor]) -> None:
+    """Write the quantized buffers of ``modules`` (name -> QuantLinear, QuantMLP, or a plain tensor
+    such as a norm gain) to ``path``."""
     tensors: dict[str, torch.Tensor] = {}
     meta = {"format": FORMAT}
     for name, m in modules.items():
@@ -51,8 +52,11 @@ def save_quantized(path: str, modules: Mapping[str, nn.Module]) -> None:
             _linear_tensors(f"{name}.down_proj", m.down_proj, tensors)
             meta[name] = json.dumps({"kind": "mlp", "mode": m.mode, "hidden": m.hidden_size,
                                      "intermediate": m.intermediate_size, "gate_up_layout": GATE_UP_LAYOUT})
+        elif isinstance(m, torch.Tensor):
+            tensors[name] = m.detach().contiguous().cpu()
+            meta[name] = json.dumps({"kind": "tensor"})
         else:
-            raise ValueError(f"{name!r}: only QuantLinear and QuantMLP modules are stored, got {type(m).__name__}")
+            raise ValueError(f"{name!r}: only QuantLinear, QuantMLP and tensors are stored, got {type(m).__name__}")
     save_file(tensors, path, metadata=meta)
 
 
@@ -69,9 +73,11 @@ def _fill(lin: QuantLinear, handle: Any, prefix: str) -> None:
         lin.weight_scale.copy_(s)
 
 
-def load_quantized(path: str, *, dtype: torch.dtype = torch.bfloat16, device: Any = "cuda") -> dict[str, nn.Module]:
-    """Modules stored by :func:`save_quantized`, built with output ``dtype`` on ``device``."""
-    out: dict[str, nn.Module] = {}
+def load_quantized(path: str, *, dtype: torch.dtype = torch.bfloat16,
+                   device: Any = "cuda") -> dict[str, nn.Module | torch.Tensor]:
+    """Modules stored by :func:`save_quantized`, built with output ``dtype`` on ``device`` (plain
+    tensors come back as stored, on ``device``)."""
+    out: dict[str, nn.Module | torch.Tensor] = {}
     with safe_open(path, framework="pt") as handle:
         meta = handle.metadata() or {}
         if meta.get("format") != FORMAT:
@@ -89,6 +95,8 @@ def load_quantized(path: str, *, dtype: torch.dtype = torch.bfloat16, device: An
                 m = QuantMLP(info["hidden"], info["intermediate"], mode=info["mode"], dtype=dtype, device=device)
                 _fill(m.gate_up_proj, handle, f"{name}.gate_up_proj")
                 _fill(m.down_proj, handle, f"{name}.down_proj")
+            elif info["kind"] == "tensor":
+                m = handle.get_tensor(name).to(device)
             else:
                 raise ValueError(f"{name}: unknown module kind {info['kind']!r}")
             out[name] = m
