@@ -6,6 +6,9 @@
 #include <stdio.h>
 #include <stdarg.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "../../include/d3w8a8.h"
@@ -34,6 +37,39 @@ bool mode_ok(int m) { return m == D3W8A8_INT8 || m == D3W8A8_FP8; }
 bool dtype_ok(int d) { return d == D3W8A8_BF16 || d == D3W8A8_F16 || d == D3W8A8_F32; }
 int esize(int d) { return d == D3W8A8_F32 ? 4 : 2; }
 bool aligned(const void* p, int a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
+
+// Split-K scratch of d3w8a8_gemm_noalloc: device memory of the library's own code object, one copy
+// per GPU, held until the process ends. In host code `scratch` names a host-side stand-in, not the
+// device array: kernels and copies get the address hipGetSymbolAddress returns for the current
+// device (scratch_device_ptr), never the name.
+constexpr int64_t kScratchBytes = D3W8A8_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The scratch array's address on the current device, looked up once per device (with that device
+// current, as every later call on it is).
+int scratch_device_ptr(void** out) {
+  int dev = 0;
+  const hipError_t ge = hipGetDevice(&dev);
+  if (ge != hipSuccess) return fail(D3W8A8_EHIP, "gemm_noalloc: hipGetDevice: %s", hipGetErrorString(ge));
+  if (dev < 0 || dev >= kMaxDevices) return fail(D3W8A8_EINVAL, "gemm_noalloc: device %d beyond %d", dev, kMaxDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p)
+        return fail(D3W8A8_EHIP, "gemm_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return D3W8A8_OK;
+}
 
 }  // namespace
 
@@ -233,6 +269,24 @@ int d3w8a8_gemm_ws(int mode, const void* a, int64_t lda, const float* a_scale, c
                    int ksplit, void* workspace, int64_t workspace_bytes, void* stream) {
   return gemm_impl(mode, a, lda, a_scale, w, ldw, w_scale, M, N, K, epilogue, out_dtype, out, ldo, res, ldr,
                    row_amax, row_map, tile, ksplit, workspace, workspace_bytes, stream);
+}
+
+int d3w8a8_gemm_noalloc(int mode, const void* a, int64_t lda, const float* a_scale, const void* w, int64_t ldw,
+                        const float* w_scale, int64_t M, int64_t N, int64_t K, int epilogue, int out_dtype, void* out,
+                        int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
+                        int ksplit, void* stream) {
+  if (ksplit > 1 && M > 0 && N > 0 && K > 0 && K % 16 == 0 && lda >= K && ldw >= K && M <= INT32_MAX / 2 &&
+      N <= INT32_MAX / 2 && tile >= D3W8A8_TILE_AUTO && tile <= D3W8A8_TILE_DMA_256x192_W4) {
+    // an explicit split larger than the scratch: name both sizes rather than the generic plan error
+    const d3::GemmPlan want = d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, INT64_MAX, epilogue);
+    if (!want.error && want.ws_bytes > kScratchBytes)
+      return fail(D3W8A8_EINVAL, "gemm_noalloc: ksplit %d needs %lld bytes of split-K scratch; the library holds %lld",
+                  ksplit, (long long)want.ws_bytes, (long long)kScratchBytes);
+  }
+  void* ws = nullptr;
+  if (const int rc = scratch_device_ptr(&ws)) return rc;
+  return gemm_impl(mode, a, lda, a_scale, w, ldw, w_scale, M, N, K, epilogue, out_dtype, out, ldo, res, ldr,
+                   row_amax, row_map, tile, ksplit, ws, kScratchBytes, stream);
 }
 
 int64_t d3w8a8_gemm_workspace(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,

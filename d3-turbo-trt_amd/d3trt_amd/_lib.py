@@ -21,6 +21,7 @@ EPI_DEQUANT, EPI_RAW, EPI_SWIGLU, EPI_RESIDUAL = 0, 1, 2, 3
 TILE_AUTO, TILE_256, TILE_128, TILE_64x128 = -1, 0, 1, 2
 MAX_SEGMENTS = 256  # D3W8A8_MAX_SEGMENTS: blocks of one ragged batch
 KSPLIT_AUTO = -1  # D3W8A8_KSPLIT_AUTO
+NOALLOC_SCRATCH_BYTES = 16 << 20  # D3W8A8_NOALLOC_SCRATCH_BYTES: split-K scratch of d3w8a8_gemm_noalloc
 TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4 = 3, 4, 5, 6
 TILE_DMA_128_W4_K128 = 7  # 128-byte K steps: K % 128 == 0
 TILE_DMA_256x192_W4 = 8  # 3 column blocks per wave: not for the SwiGLU epilogue
@@ -54,6 +55,8 @@ SIGNATURES = {
                     _p, _i32, _p],
     "d3w8a8_gemm_ws": [_i32, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p, _i64, _p,
                        _p, _i32, _i32, _p, _i64, _p],
+    "d3w8a8_gemm_noalloc": [_i32, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p, _i64,
+                            _p, _p, _i32, _i32, _p],
 }
 # name -> argtypes of the entry points that return int64
 INT64_FUNCS = {

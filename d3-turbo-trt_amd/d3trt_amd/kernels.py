@@ -221,12 +221,15 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
          out_dtype: torch.dtype = torch.bfloat16, out: Optional[torch.Tensor] = None,
          residual: Optional[torch.Tensor] = None, row_amax: Optional[torch.Tensor] = None,
          row_map: Optional[torch.Tensor] = None, tile: int = _lib.TILE_AUTO,
-         ksplit: int = _lib.KSPLIT_AUTO) -> torch.Tensor:
+         ksplit: int = _lib.KSPLIT_AUTO, noalloc: bool = False) -> torch.Tensor:
     """W8A8 GEMM ``a @ w.T`` with a fused epilogue (see include/d3w8a8.h).
 
     Skinny problems may split K over several workgroups per output tile
     (``ksplit``, automatic by default); the split-K workspace is this module's
-    per-(device, stream) buffer from :func:`workspace`.
+    per-(device, stream) buffer from :func:`workspace`. With ``noalloc=True``
+    the partial sums go to the library's static per-GPU scratch instead
+    (``d3w8a8_gemm_noalloc``: nothing is allocated for them; such calls on one
+    GPU must run in order).
     """
     a = _rows(a, "a")
     w = _rows(w, "w")
@@ -278,6 +281,14 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
             raise ValueError("dequantizing epilogues need a_scale [M] and w_scale [N]")
     lib = _lib.load()
     st = _stream(a)
+    if noalloc:
+        rc = lib.d3w8a8_gemm_noalloc(
+            mode_code(mode), a.data_ptr(), a.stride(0), _ptr(a_scale), w.data_ptr(), w.stride(0), _ptr(w_scale),
+            M, N, K, epilogue, dtype_code(odt) if epilogue != _lib.EPI_RAW else 0, out.data_ptr(), out.stride(0),
+            _ptr(residual), residual.stride(0) if residual is not None else 0, _ptr(row_amax), _ptr(row_map),
+            tile, ksplit, st)
+        _lib.check(rc, "gemm_noalloc")
+        return out
     ws = None
     if ksplit != 1:
         # only a plan that splits K touches the workspace (the state-pass shapes never do)

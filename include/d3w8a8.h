@@ -158,6 +158,25 @@ int d3w8a8_gemm_ws(int mode, const void* a, int64_t lda, const float* a_scale, c
                    int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
                    int ksplit, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* d3w8a8_gemm_ws without a workspace argument: the split-K partial sums go to
+ * the library's own scratch, a static device array of
+ * D3W8A8_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends).
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc); the call itself allocates nothing. Same operation,
+ * arguments and results as d3w8a8_gemm_ws given a workspace of that size
+ * (ksplit AUTO picks a split that fits it; an explicit ksplit that needs more
+ * returns D3W8A8_EINVAL). Every call on one GPU uses that GPU's one scratch
+ * array, so calls on one GPU must be ordered (one stream): calls that overlap
+ * race on it. The stream's device must be current. Nothing needs clearing
+ * between calls: each split overwrites its whole slot before the reduce
+ * reads it. */
+#define D3W8A8_NOALLOC_SCRATCH_BYTES (16 << 20)
+int d3w8a8_gemm_noalloc(int mode, const void* a, int64_t lda, const float* a_scale, const void* w, int64_t ldw,
+                        const float* w_scale, int64_t M, int64_t N, int64_t K, int epilogue, int out_dtype, void* out,
+                        int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
+                        int ksplit, void* stream);
+
 /* Workspace bytes d3w8a8_gemm_ws uses for this problem, tile and ksplit when
  * given at most `max_bytes` (0 when it would not split); -1 on bad arguments. */
 int64_t d3w8a8_gemm_workspace(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
