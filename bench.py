@@ -154,10 +154,11 @@ def read_traffic():
     return out
 
 
-def launch_us(fn_of, n_launches: int, rounds: int = 3) -> float:
-    """Average duration (us) of back-to-back launches fn_of(0), ..., fn_of(n_launches - 1): the launches
+def launch_us(fn_of, n_launches: int, rounds: int = 21) -> float:
+    """Duration (us) per launch of back-to-back launches fn_of(0), ..., fn_of(n_launches - 1): the launches
     are captured once in a HIP graph, whose replay is timed between two HIP events on the current stream
-    (the stream the kernels run on), so host latency never leaves the GPU waiting. Best of `rounds`."""
+    (the stream the kernels run on), so host latency never leaves the GPU waiting. The median over
+    `rounds` replays (at least 20)."""
     import torch
 
     cur = torch.cuda.current_stream()
@@ -172,17 +173,18 @@ def launch_us(fn_of, n_launches: int, rounds: int = 3) -> float:
             fn_of(i)
     graph.replay()
     torch.cuda.synchronize()
-    best = float("inf")
-    for _ in range(rounds):
+    times = []
+    for _ in range(max(rounds, 20)):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
         graph.replay()
         e1.record()
         torch.cuda.synchronize()
-        best = min(best, e0.elapsed_time(e1) * 1e3 / n_launches)
+        times.append(e0.elapsed_time(e1) * 1e3 / n_launches)
     del graph
-    return best
+    times.sort()
+    return times[len(times) // 2]
 
 
 ROTATE_BYTES = 320 << 20  # > the 256 MB Infinity Cache: rotated operands come from HBM
@@ -326,7 +328,13 @@ def run_single_linear(args):
     # device time: the forward's two launches, back to back in a graph (host latency excluded)
     dev_us = launch_us(lambda i: lin(x), 50)
     byts = quant_bytes(M, K) + gemm_bytes(M, N, K)
+    cpu = None
+    if not args.no_cpu:
+        xc, wq, ws = x.cpu(), lin.weight.cpu(), lin.weight_scale.cpu()
+        cpu = cpu_rate(lambda: R.emulated_linear(xc, wq, ws, "int8", torch.bfloat16), 2.0 * M * N * K, 2.0,
+                       "the whole workload: oracle emulated_linear (quant.py:158-162), 128 x 1024 x 1024")
     return {
+        "cpu_baseline": cpu,
         "shape": f"{M}x{N}x{K}", "mode": "int8", "forward_us": round(fwd_ms * 1e3, 2),
         "forward_note": "eager module call timed by an event pair: host latency included",
         "device_us": round(dev_us, 2),
@@ -352,17 +360,29 @@ def run_ragged(args):
         x[b, :n] = R.outlier_activations(g, n, K)
     x = x.to(dev)
     T = sum(lengths)
-    out = {"lengths": lengths, "rows": T, "shapes": {}}
+    out = {"lengths": lengths, "rows": T, "shapes": {},
+           "timing": "graph replay of back-to-back forward_ragged calls (ragged quantize + one GEMM each), "
+                     "median of >= 20 replays"}
+    cpu_work = []
     for N in (6144, 4096, 24576):
         lin = QuantLinear(K, N, mode="int8", dtype=torch.bfloat16, device=dev)
         lin.load_full(R.gaussian_weight(g, N, K).to(dev))
-        ms, timer = timed_steps(lambda t: _call(t, "fwd", lambda: lin.forward_ragged(x, lengths)),
-                                args.steps, args.warmup)
-        f_ms = timer.ms("fwd")
+        us = launch_us(lambda i: lin.forward_ragged(x, lengths), 8)
         ops = 2.0 * T * N * K
-        out["shapes"][f"N{N}"] = {"ms": round(f_ms, 4), "tops": round(ops / (f_ms * 1e-3) / 1e12, 1),
-                                  "frac_peak": round(ops / (f_ms * 1e-3) / 1e12 / PEAK_TOPS["int8"], 4)}
+        out["shapes"][f"N{N}"] = {"us": round(us, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1),
+                                  "frac_peak": round(ops / (us * 1e-6) / 1e12 / PEAK_TOPS["int8"], 4)}
+        if not args.no_cpu:
+            cpu_work.append((lin.weight.cpu(), lin.weight_scale.cpu()))
         del lin
+    if cpu_work:
+        xb = [x[b, :n].cpu() for b, n in enumerate(lengths[:2])]  # the first two blocks of the batch
+        rows = sum(t.shape[0] for t in xb)
+        ops = sum(2.0 * rows * wq.shape[0] * K for wq, _ in cpu_work)
+        full = sum(2.0 * T * wq.shape[0] * K for wq, _ in cpu_work)
+        out["cpu_baseline"] = cpu_rate(
+            lambda: [R.emulated_linear(xi, wq, ws, "int8", torch.bfloat16) for wq, ws in cpu_work for xi in xb],
+            ops, 3.0, f"the first 2 of the 16 blocks ({rows} rows) through the three projections, block by "
+                      "block (the reference runs them right-padded, backends/trtllm.py:149-179)", full)
     return out
 
 
@@ -450,6 +470,18 @@ def run_mlp_block(args):
     rq = 2 * M * I + M * I + 4 * M
     k["requant"] = {"us": round(us, 2), "gbs": round(rq / (us * 1e-6) / 1e9, 1),
                     "frac_hbm": round(rq / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+    # reference for the HBM-bound kernels: torch's bf16 -> e4m3 cast of the same shapes moves the same
+    # bytes (2 read + 1 written per element) with no row reduction, inputs rotated over > 256 MB
+    for name, cols in (("reference_cast_4096x4096", H), ("reference_cast_4096x12288", I)):
+        n_c = max(2, -(-ROTATE_BYTES // (M * cols * 2)))
+        srcs = [torch.randn(M, cols, device=dev).to(torch.bfloat16) for _ in range(n_c)]
+        dst = torch.empty(M, cols, dtype=torch.float8_e4m3fn, device=dev)
+        us = launch_us(lambda i: dst.copy_(srcs[i % n_c]), 4 * n_c)
+        byts = 3 * M * cols
+        k[name] = {"us": round(us, 2), "gbs": round(byts / (us * 1e-6) / 1e9, 1),
+                   "frac_hbm": round(byts / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                   "what": "torch bf16->float8_e4m3fn copy_, same bytes as a quantize, no row reduction"}
+        del srcs
     n_w = max(2, -(-ROTATE_BYTES // dn.weight.numel()))
     wds = [dn.weight.clone() for _ in range(n_w)]
     out = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
@@ -460,7 +492,17 @@ def run_mlp_block(args):
     k["down_residual"] = {"us": round(us, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1),
                           "frac_peak": round(ops / (us * 1e-6) / 1e12 / PEAK_TOPS["int8"], 4)}
     total_ops = 2.0 * M * (2 * I) * H + 2.0 * M * H * I
-    return {"ms": round(ms, 4), "tops": round(total_ops / (ms * 1e-3) / 1e12, 1),
+    cpu = None
+    if not args.no_cpu:
+        rows = 32
+        xs, nwc = x[:rows].cpu(), nw.cpu()
+        wgu_q = KK.deinterleave_gate_up(gu.weight.view(torch.uint8)).view(gu.weight.dtype).cpu()
+        wgu_s = KK.deinterleave_gate_up(gu.weight_scale).cpu()
+        wd_q, wd_s = dn.weight.cpu(), dn.weight_scale.cpu()
+        cpu = cpu_rate(lambda: R.mlp_block(xs, nwc, 1e-6, wgu_q, wgu_s, wd_q, wd_s, "int8"),
+                       total_ops * rows / M, 4.0, f"{rows} of the 4096 rows through the oracle's block "
+                       "(norm, quantize, gate_up, SwiGLU, requantize, down, residual)", total_ops)
+    return {"cpu_baseline": cpu, "ms": round(ms, 4), "tops": round(total_ops / (ms * 1e-3) / 1e12, 1),
             "step": "one HIP graph replay (checked equal to the eager block)",
             "ms_eager": round(ms_eager, 4), "kernels": k,
             "kernel_timing": "graph replay of back-to-back launches between HIP events; inputs / weights rotated "
@@ -566,15 +608,119 @@ def run_linear_stack(args):
     res["total_ms_b255"] = round(res["state_ms"] + res["questions_b255_ms"], 3)
     weight_bytes = layers * ((6144 + 4096 + 24576) * 4096 + 4096 * 12288)  # 8-bit weights of one sweep
     res["weight_bytes_per_sweep"] = weight_bytes
+    res["questions_b8_weight_gbs"] = round(weight_bytes * -(-nq // 8) / (res["questions_b8_ms"] * 1e-3) / 1e9, 1)
+    res["per_shape"] = stack_per_shape(stack, gen)
+    if not args.no_cpu:
+        from d3trt_amd import kernels as KK
+        from oracle import quant_ref as R
+
+        lay = stack.layers[0]
+        gu = lay.mlp.gate_up_proj
+        w = dict(w_in=lay.input_layernorm.cpu(), w_post=lay.post_attention_layernorm.cpu(),
+                 wqkv_q=lay.qkv_proj.weight.cpu(), wqkv_s=lay.qkv_proj.weight_scale.cpu(),
+                 wo_q=lay.o_proj.weight.cpu(), wo_s=lay.o_proj.weight_scale.cpu(),
+                 wgu_q=KK.deinterleave_gate_up(gu.weight.view(torch.uint8)).view(gu.weight.dtype).cpu(),
+                 wgu_s=KK.deinterleave_gate_up(gu.weight_scale).cpu(),
+                 wd_q=lay.mlp.down_proj.weight.cpu(), wd_s=lay.mlp.down_proj.weight_scale.cpu())
+        rows = 8
+        xs = state[:rows].cpu()
+        per_token_layer = 2.0 * 4096 * (6144 + 4096 + 24576) + 2.0 * 12288 * 4096
+        full = per_token_layer * layers * (8192 + nq * qlen)
+        res["cpu_baseline"] = cpu_rate(lambda: R.stack_layer(xs, mode="fp8", **w), per_token_layer * rows, 4.0,
+                                       f"{rows} tokens through one layer of the oracle's FP8 stack (float64 "
+                                       f"products); the projection covers {layers} layers x (8192 state + "
+                                       f"{nq * qlen} question tokens)", full)
     del stack
     torch.cuda.empty_cache()
     return res
 
 
+def stack_per_shape(stack, gen) -> dict:
+    """Each launch of a stack layer alone, at the state pass's M = 8192 and a question batch's M = 128:
+    back-to-back launches over the stack's own layers (each launch brings its layer's weights from HBM),
+    replayed from a HIP graph, median of >= 20 replays. GEMMs against the FP8 MFMA peak at M = 8192 and
+    against HBM at M = 128; the quantize kernels against HBM."""
+    import torch
+
+    from d3trt_amd import _lib
+    from d3trt_amd import kernels as KK
+
+    dev = next(stack.buffers()).device
+    L = stack.layers
+    n = len(L)
+    H, Q, I = 4096, 6144, 12288
+    lib = _lib.load()
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    out = {}
+    for M in (8192, 128):
+        x = torch.randn(M, H, generator=gen, device=dev).to(torch.bfloat16)
+        q_in = (torch.randn(M, I, generator=gen, device=dev) * 8).to(torch.float8_e4m3fn)
+        s_in = torch.rand(M, generator=gen, device=dev) * 1e-3
+        qkv = torch.empty(M, Q, dtype=torch.bfloat16, device=dev)
+        hbuf = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+        amax = torch.zeros(M, dtype=torch.float32, device=dev)
+        o = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+        qb = torch.empty(M, I, dtype=torch.float8_e4m3fn, device=dev)
+        sb = torch.empty(M, dtype=torch.float32, device=dev)
+        a4 = q_in[:, :H]
+        gemms = {
+            "qkv": (lambda i: KK.gemm("fp8", a4, s_in, L[i % n].qkv_proj.weight, L[i % n].qkv_proj.weight_scale,
+                                      out=qkv), Q, H, 0),
+            "o_proj+residual": (lambda i: KK.gemm("fp8", a4, s_in, L[i % n].o_proj.weight,
+                                                  L[i % n].o_proj.weight_scale, out=o, residual=x,
+                                                  epilogue=_lib.EPI_RESIDUAL), H, H, 1),
+            "gate_up+swiglu": (lambda i: KK.gemm("fp8", a4, s_in, L[i % n].mlp.gate_up_proj.weight,
+                                                 L[i % n].mlp.gate_up_proj.weight_scale, out=hbuf, row_amax=amax,
+                                                 epilogue=_lib.EPI_SWIGLU), 2 * I, H, 0),
+            "down+residual": (lambda i: KK.gemm("fp8", q_in, s_in, L[i % n].mlp.down_proj.weight,
+                                                L[i % n].mlp.down_proj.weight_scale, out=o, residual=x,
+                                                epilogue=_lib.EPI_RESIDUAL), H, I, 1),
+        }
+        shapes = {}
+        for name, (fn, N, Kd, res_) in gemms.items():
+            us = launch_us(fn, n)
+            ops = 2.0 * M * N * Kd
+            n_out = N // 2 if "swiglu" in name else N  # SwiGLU stores half the columns
+            byts = M * Kd + N * Kd + 2 * M * n_out + 4 * (M + N) + (2 * M * N if res_ else 0)
+            e = {"us": round(us, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1),
+                 "frac_mfma": round(ops / (us * 1e-6) / 1e12 / PEAK_TOPS["fp8"], 4),
+                 "gbs": round(byts / (us * 1e-6) / 1e9, 1),
+                 "frac_hbm": round(byts / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+            e["bound"] = "mfma" if ops / byts > PEAK_TOPS["fp8"] * 1e12 / (PEAK_HBM_GBS * 1e9) else "hbm"
+            shapes[name] = e
+        xs = [torch.randn(M, H, generator=gen, device=dev).to(torch.bfloat16) for _ in range(4)]
+        hs = [torch.randn(M, I, generator=gen, device=dev).to(torch.bfloat16) for _ in range(2)]
+        amax_h = torch.full((M,), 4.0, device=dev)
+        quant = {
+            "norm+quantize": (lambda i: _lib.check(lib.d3w8a8_rmsnorm_quantize(
+                1, 0, xs[i % 4].data_ptr(), H, 0, L[i % n].input_layernorm.data_ptr(), M, H, 1e-6, 1,
+                qb.data_ptr(), H, sb.data_ptr(), None, 0, None, st()), "norm"), quant_bytes(M, H) + 2 * H),
+            "quantize(q block)": (lambda i: _lib.check(lib.d3w8a8_quantize_rows(
+                1, 0, xs[i % 4].data_ptr(), H, M, H, qb.data_ptr(), H, sb.data_ptr(), st()), "quant"),
+                quant_bytes(M, H)),
+            "requantize(h)": (lambda i: _lib.check(lib.d3w8a8_quantize_rows_amax(
+                1, 0, hs[i % 2].data_ptr(), I, amax_h.data_ptr(), M, I, qb.data_ptr(), I, sb.data_ptr(), st()),
+                "requant"), quant_bytes(M, I)),
+        }
+        for name, (fn, byts) in quant.items():
+            us = launch_us(fn, 16)
+            shapes[name] = {"us": round(us, 2), "gbs": round(byts / (us * 1e-6) / 1e9, 1),
+                            "frac_hbm": round(byts / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "bound": "hbm"}
+        out[f"M{M}"] = shapes
+        del x, q_in, qkv, hbuf, o, qb, xs, hs
+        torch.cuda.empty_cache()
+    out["note"] = ("M8192: the state pass's launches, GEMMs against the 5.0 PF FP8 peak; M128: a question batch "
+                   "of 8 x 16 tokens, GEMMs against 8 TB/s (weights streamed); back-to-back over the stack's "
+                   "layers (weights from HBM), median of >= 20 graph replays")
+    return out
+
+
 def run_question_gemms(args):
     """The four projections at question-batch M = 128 (8 blocks x 16 tokens), FP8: HBM-bound weight
-    streams. Each call reads a different weight copy from a pool of > 600 MB, so no call finds its
-    weights in the 256 MB Infinity Cache; weight GB/s and algorithmic GB/s against 8 TB/s."""
+    streams. Back-to-back launches replayed from a HIP graph, each reading a different weight copy from a
+    pool of > 600 MB, so no launch finds its weights in the 256 MB Infinity Cache; median of >= 20
+    replays. Weight GB/s and algorithmic GB/s against 8 TB/s, for the automatic tile (weight streaming)
+    and, for comparison, the 128x128 split-K tile."""
     import torch
 
     from d3trt_amd import _lib
@@ -583,7 +729,6 @@ def run_question_gemms(args):
     dev = torch.device("cuda:0")
     M, out = 128, {}
     gen = torch.Generator(device=dev).manual_seed(0)
-    lib = _lib.load()
     for name, (N, Kd) in (("qkv", (6144, 4096)), ("o_proj", (4096, 4096)), ("gate_up", (24576, 4096)),
                           ("down", (4096, 12288))):
         copies = max(2, -(-(600 << 20) // (N * Kd)))
@@ -592,34 +737,47 @@ def run_question_gemms(args):
         a = (torch.randn(M, Kd, generator=gen, device=dev) * 8).to(torch.float8_e4m3fn)
         a_s = torch.rand(M, generator=gen, device=dev) * 1e-3
         y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-        calls = 4 * copies
-        for i in range(copies):
-            K.gemm("fp8", a, a_s, ws[i], w_s, out=y)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(calls):
-            K.gemm("fp8", a, a_s, ws[i % copies], w_s, out=y)
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) / calls * 1e3
-        ws_bytes = lib.d3w8a8_gemm_workspace(M, N, Kd, Kd, Kd, -1, -1, K.WORKSPACE_BYTES)
-        tiles = ((M + 127) // 128) * ((N + 127) // 128)
-        out[name] = {"M": M, "N": N, "K": Kd, "us": round(us, 2),
-                     "weight_gbs": round(N * Kd / (us * 1e-6) / 1e9, 1),
-                     "algo_gbs": round(gemm_bytes(M, N, Kd) / (us * 1e-6) / 1e9, 1),
-                     "frac_hbm": round(gemm_bytes(M, N, Kd) / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 3),
-                     "ksplit": ws_bytes // (tiles * 128 * 128 * 4) if ws_bytes > 0 else 1}
+        res = {"M": M, "N": N, "K": Kd}
+        for label, tile in (("", _lib.TILE_AUTO), ("splitk_tile_", _lib.TILE_DMA_128_W4_K128)):
+            us = launch_us(lambda i: K.gemm("fp8", a, a_s, ws[i % copies], w_s, out=y, tile=tile), 2 * copies)
+            res[label + "us"] = round(us, 2)
+            res[label + "frac_hbm"] = round(gemm_bytes(M, N, Kd) / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 3)
+            if not label:
+                res["weight_gbs"] = round(N * Kd / (us * 1e-6) / 1e9, 1)
+                res["algo_gbs"] = round(gemm_bytes(M, N, Kd) / (us * 1e-6) / 1e9, 1)
+        out[name] = res
         del ws
         torch.cuda.empty_cache()
-    out["note"] = ("per-call HIP-event time, weights rotated over > 600 MB; tile 7 (128-byte K steps) with "
-                   "automatic split-K; includes the split-K reduce launch")
+    out["note"] = ("graph replay of back-to-back launches (median of >= 20), weights rotated over > 600 MB; "
+                   "automatic tile = weight streaming (no split-K); splitk_tile_* = the 128x128 tile with "
+                   "128-byte K steps and its automatic split-K (partials + reduce launch)")
     return out
 
 
 # ---------------------------------------------------------------------------------------------
 # CPU baseline: the oracle's restatement of the reference CPU path
 # ---------------------------------------------------------------------------------------------
+def cpu_rate(fn, ops: float, seconds: float, sample: str, full_ops: float | None = None) -> dict:
+    """Time fn() (the oracle on the host cores) for about `seconds`; report its TOPS on `ops` per call and,
+    given the full workload's ops, the projected time of the whole configuration."""
+    import torch
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        if time.perf_counter() - t0 > seconds:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    out = {"value": round(ops / dt / 1e12, 4), "unit": "TOPS", "cores": torch.get_num_threads(), "kind": "port",
+           "sample": f"{sample}; {reps} reps ({time.perf_counter() - t0:.1f} s); host {_cpu_model()}"}
+    if full_ops is not None:
+        out["projected_full_ms"] = round(full_ops / (ops / dt) * 1e3, 1)
+    return out
+
+
 def cpu_baseline_state_pass(layers, mode: str, rows: int, seconds: float):
     """QuantLinear._emulated (quant.py:158-162, restated by the oracle) on `rows` rows of each
     state-pass shape, repeated for about `seconds` of wall time on every host core."""
@@ -692,6 +850,9 @@ def main() -> int:
     ap.add_argument("--stack-layers", type=int, default=48)
     ap.add_argument("--single", action="store_true",
                     help="run a 1 GiB calibration copy, then one untimed step (for rocprofv3 --pmc passes)")
+    ap.add_argument("--config", default=None,
+                    help="run only this entry of `configs` (no headline step) and print it: for profiling one "
+                         "workload, e.g. question_gemms_fp8_m128")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -707,14 +868,22 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.single:
         return single_pass(args.mode)
+    workloads = (("single_int8_linear", run_single_linear), ("ragged_int8", run_ragged),
+                 ("mlp_block_int8", run_mlp_block), ("gated_o_proj_quant_fp8", run_gated_quant),
+                 ("gdn_norm_quant_fp8", run_gdn_norm_quant),
+                 ("question_gemms_fp8_m128", run_question_gemms),
+                 ("linear_stack_fp8", run_linear_stack))
+    if args.config:
+        fns = dict(workloads)
+        if args.config not in fns:
+            print(json.dumps({"error": f"unknown config {args.config!r}", "configs": list(fns)}))
+            return 2
+        print(json.dumps({"config": args.config, "result": fns[args.config](args)}))
+        return 0
     result, layers = run_state_pass(args, args.mode)
     if not args.headline_only:
         configs = {}
-        for name, fn in (("single_int8_linear", run_single_linear), ("ragged_int8", run_ragged),
-                         ("mlp_block_int8", run_mlp_block), ("gated_o_proj_quant_fp8", run_gated_quant),
-                         ("gdn_norm_quant_fp8", run_gdn_norm_quant),
-                         ("question_gemms_fp8_m128", run_question_gemms),
-                         ("linear_stack_fp8", run_linear_stack)):
+        for name, fn in workloads:
             configs[name] = fn(args)
             print(json.dumps({"progress": name, "done": True}), file=sys.stderr, flush=True)
         result["configs"] = configs

@@ -219,7 +219,7 @@ static int gemm_impl(int mode, const void* a, int64_t lda, const float* a_scale,
   if (epilogue < D3W8A8_EPI_DEQUANT || epilogue > D3W8A8_EPI_RESIDUAL)
     return fail(D3W8A8_EINVAL, "gemm: unknown epilogue %d", epilogue);
   if (epilogue != D3W8A8_EPI_RAW && !dtype_ok(out_dtype)) return fail(D3W8A8_EINVAL, "gemm: unknown out dtype");
-  if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_256x192_W4) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
+  if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_WS) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
   if (ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) return fail(D3W8A8_EINVAL, "gemm: bad ksplit %d", ksplit);
   if (workspace_bytes < 0 || (workspace_bytes > 0 && (!workspace || !aligned(workspace, 256))))
     return fail(D3W8A8_EINVAL, "gemm: the workspace must be 256-byte aligned device memory");
@@ -276,7 +276,7 @@ int d3w8a8_gemm_noalloc(int mode, const void* a, int64_t lda, const float* a_sca
                         int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
                         int ksplit, void* stream) {
   if (ksplit > 1 && M > 0 && N > 0 && K > 0 && K % 16 == 0 && lda >= K && ldw >= K && M <= INT32_MAX / 2 &&
-      N <= INT32_MAX / 2 && tile >= D3W8A8_TILE_AUTO && tile <= D3W8A8_TILE_DMA_256x192_W4) {
+      N <= INT32_MAX / 2 && tile >= D3W8A8_TILE_AUTO && tile <= D3W8A8_TILE_WS) {
     // an explicit split larger than the scratch: name both sizes rather than the generic plan error
     const d3::GemmPlan want = d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, INT64_MAX, epilogue);
     if (!want.error && want.ws_bytes > kScratchBytes)
@@ -292,7 +292,7 @@ int d3w8a8_gemm_noalloc(int mode, const void* a, int64_t lda, const float* a_sca
 int64_t d3w8a8_gemm_workspace(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
                               int64_t max_bytes) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 16 || lda < K || ldw < K || M > INT32_MAX / 2 || N > INT32_MAX / 2 ||
-      tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_DMA_256x192_W4 || ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) {
+      tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_WS || ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) {
     fail(D3W8A8_EINVAL, "gemm_workspace: bad arguments");
     return -1;
   }

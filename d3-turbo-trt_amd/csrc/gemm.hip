@@ -76,6 +76,7 @@ TileShape shape_of(int tile) {
     case kDma256x128w4: return {256, 128, true, 64};
     case kDma128w4k128: return {128, 128, true, 128};
     case kDma256x192w4: return {256, 192, true, 64};
+    case kWs: return {128, 32, true, 128};
   }
   return {0, 0, false, 0};
 }
@@ -101,7 +102,9 @@ int64_t rounds(int64_t tiles, int64_t cus) { return (tiles + cus - 1) / cus; }
 // epilogues without gate/up pairs). Measured: 1440 x 6144 x 4096 INT8 70.0 ->
 // 60.6 us; 1280 rows keep 256x128 (44.2 us, 256x192 52.5 us), as the rule says. M <= 128 (a
 // 256-row tile would compute half its rows for nothing) streams the weights:
-// 128x128 with 128-byte K steps when K allows. Tile counts are weighed against
+// 128x128 with 128-byte K steps when K allows, split over K by the planner
+// (measured on MI355X at M = 128 it beats the weight-streaming kernel of
+// gemm_ws.hpp, tile kWs, on QKV, gate_up and down; kWs is taken on request). Tile counts are weighed against
 // the device's compute units (`cus`; the thresholds were measured on 256).
 int choose_tile(int64_t M, int64_t N, int64_t K, bool fit, int epi, int64_t cus) {
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);

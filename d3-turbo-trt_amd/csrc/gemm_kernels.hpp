@@ -950,6 +950,9 @@ static hipError_t launch_dma(GemmParams p, hipStream_t st) {
 }
 
 template <int MODE, int EPI, int OUT>
+static hipError_t launch_ws(GemmParams p, hipStream_t st);  // gemm_ws.hpp
+
+template <int MODE, int EPI, int OUT>
 hipError_t launch_epi(GemmParams p, int tile, hipStream_t st) {
   if (p.ksplit < 1 || (p.ksplit > 1 && tile < kDma256w8)) return hipErrorInvalidValue;
   switch (tile) {
@@ -964,8 +967,11 @@ hipError_t launch_epi(GemmParams p, int tile, hipStream_t st) {
     case kDma256x192w4:
       if constexpr (EPI == kEpiSwiGLU) return hipErrorInvalidValue;  // 3 column blocks per wave: no gate/up pairs
       else return launch_dma<MODE, 256, 192, 2, 2, EPI, OUT>(p, st);
+    case kWs: return launch_ws<MODE, EPI, OUT>(p, st);
   }
   return hipErrorInvalidValue;
 }
 
 }  // namespace d3
+
+#include "gemm_ws.hpp"

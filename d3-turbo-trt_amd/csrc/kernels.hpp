@@ -68,7 +68,8 @@ enum TileCfg : int {
   kDma256x128w4 = 6, // DMA pipeline 256x128, 4 waves (128x64 each), 4 stages
   kDma128w4k128 = 7, // DMA pipeline 128x128, 4 waves, 128-byte K steps (weight streaming, K % 128 == 0)
   kDma256x192w4 = 8, // DMA pipeline 256x192, 4 waves (128x96 each), 4 stages; not for SwiGLU
-  kTileCount = 9
+  kWs = 9,           // weight streaming for skinny M: 32- or 64-column slabs, waves split K (K % 128 == 0)
+  kTileCount = 10
 };
 
 constexpr int kMaxKSplit = 32;

@@ -25,15 +25,16 @@ NOALLOC_SCRATCH_BYTES = 16 << 20  # D3W8A8_NOALLOC_SCRATCH_BYTES: split-K scratc
 TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4 = 3, 4, 5, 6
 TILE_DMA_128_W4_K128 = 7  # 128-byte K steps: K % 128 == 0
 TILE_DMA_256x192_W4 = 8  # 3 column blocks per wave: not for the SwiGLU epilogue
+TILE_WS = 9  # weight streaming for skinny M: K % 128 == 0, never splits K
 TILES = (TILE_256, TILE_128, TILE_64x128, TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4,
-         TILE_DMA_128_W4_K128, TILE_DMA_256x192_W4)
+         TILE_DMA_128_W4_K128, TILE_DMA_256x192_W4, TILE_WS)
 DMA_TILES = (TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4, TILE_DMA_128_W4_K128,
-             TILE_DMA_256x192_W4)
+             TILE_DMA_256x192_W4, TILE_WS)
 
 
 def tile_k_multiple(tile: int) -> int:
     """K must be a multiple of this for `tile` (16 for the register-staged tiles)."""
-    return 128 if tile == TILE_DMA_128_W4_K128 else 64 if tile in DMA_TILES else 16
+    return 128 if tile in (TILE_DMA_128_W4_K128, TILE_WS) else 64 if tile in DMA_TILES else 16
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64

@@ -140,13 +140,19 @@ def test_split_k_plan_on_the_host():
     lib = _lib.load()
     big = 64 << 20
     slot = 128 * 128 * 4
-    # 128 rows x 4096 columns: 32 tiles of 128x128 leave the GPU idle -> 4 splits of 1 KiB of K each
+    k128 = _lib.TILE_DMA_128_W4_K128
+    # the weight-streaming tile never splits K
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, _lib.TILE_WS, -1, big) == 0
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, _lib.TILE_WS, 2, big) == -1
+    # the automatic tile at question-batch M is the 128x128 one with 128-byte steps, split as below
     assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, big) == 32 * 4 * slot
+    # on the 128x128 tile, 128 rows x 4096 columns: 32 tiles leave the GPU idle -> 4 splits of 1 KiB of K
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, k128, -1, big) == 32 * 4 * slot
     # down projection (K = 12288): 8 splits make ~one workgroup per CU
-    assert lib.d3w8a8_gemm_workspace(128, 4096, 12288, 12288, 12288, -1, -1, big) == 32 * 8 * slot
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 12288, 12288, 12288, k128, -1, big) == 32 * 8 * slot
     # a smaller workspace lowers the automatic split; none at all means no split
-    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, 32 * 3 * slot) == 32 * 3 * slot
-    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, 0) == 0
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, k128, -1, 32 * 3 * slot) == 32 * 3 * slot
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, k128, -1, 0) == 0
     # state-pass shapes fill the GPU without splitting
     assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, -1, -1, big) == 0
     # explicit requests are checked, not adjusted
@@ -159,10 +165,11 @@ def test_split_k_plan_on_the_host():
     assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, 1, 2, big) == -1  # register-staged tile
     assert b"128x128" in lib.d3w8a8_last_error()
     assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, 4, 2, big) == -1  # 256x256 tile
-    # the 256x192 tile is accepted (no split), the next tile code is not
+    # the 256x192 and weight-streaming tiles are accepted (no split), the next tile code is not
     assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, _lib.TILE_DMA_256x192_W4, -1, big) == 0
     assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, _lib.TILE_DMA_256x192_W4, 2, big) == -1
-    assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, _lib.TILE_DMA_256x192_W4 + 1, -1, big) == -1
+    assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, _lib.TILE_WS, -1, big) == 0
+    assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, _lib.TILE_WS + 1, -1, big) == -1
     dummy = 256
     assert lib.d3w8a8_gemm_ws(0, dummy, 4096, dummy, dummy, 4096, dummy, 128, 4096, 4096, 0, 0, dummy, 4096,
                               None, 0, None, None, 5, 4, dummy, 1 << 20, None) == _lib.EINVAL

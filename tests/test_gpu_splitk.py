@@ -143,15 +143,45 @@ def test_split_gemm_graph_replays(dev, mode):
     sw = torch.rand(N, generator=g).mul(1e-2).to(dev)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
+    t = _lib.TILE_DMA_128_W4_K128  # a splitting tile (the automatic one at this M streams without splits)
     with torch.cuda.stream(side):
-        eager = K.gemm(mode, a, sa, w, sw, ksplit=8).clone()
+        eager = K.gemm(mode, a, sa, w, sw, ksplit=8, tile=t).clone()
     torch.cuda.current_stream().wait_stream(side)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
-        out = K.gemm(mode, a, sa, w, sw, ksplit=8)
+        out = K.gemm(mode, a, sa, w, sw, ksplit=8, tile=t)
     for _ in range(3):
-        K.gemm(mode, a, sa, w, sw, ksplit=4)  # eager split-K work on another workspace between replays
+        K.gemm(mode, a, sa, w, sw, ksplit=4, tile=t)  # eager split-K work on another workspace between replays
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
+
+
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
+def test_gemm_captured_on_torch_default_capture_stream(dev, mode):
+    """The usual capture pattern: warm up on a side stream, then torch.cuda.graph(g) without a stream
+    (torch captures on a stream of its own). Skinny GEMMs (no split) and split-K GEMMs both capture and
+    every replay equals the eager result."""
+    g = gen(59)
+    M, N, Kd = 96, 1024, 2048
+    mk = rand_i8 if mode == "int8" else rand_fp8
+    a, w = mk(g, M, Kd).to(dev), mk(g, N, Kd).to(dev)
+    sa = torch.rand(M, generator=g).mul(1e-2).to(dev)
+    sw = torch.rand(N, generator=g).mul(1e-2).to(dev)
+    calls = [dict(), dict(tile=_lib.TILE_DMA_128_W4_K128, ksplit=4)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eager = [K.gemm(mode, a, sa, w, sw, **c).clone() for c in calls]
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [K.gemm(mode, a, sa, w, sw, **c) for c in calls]
+    for _ in range(3):
+        K.gemm(mode, a, sa, w, sw)  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o.view(torch.int16), e.view(torch.int16))
