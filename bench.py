@@ -719,8 +719,8 @@ def run_question_gemms(args):
     """The four projections at question-batch M = 128 (8 blocks x 16 tokens), FP8: HBM-bound weight
     streams. Back-to-back launches replayed from a HIP graph, each reading a different weight copy from a
     pool of > 600 MB, so no launch finds its weights in the 256 MB Infinity Cache; median of >= 20
-    replays. Weight GB/s and algorithmic GB/s against 8 TB/s, for the automatic tile (weight streaming)
-    and, for comparison, the 128x128 split-K tile."""
+    replays. Weight GB/s and algorithmic GB/s against 8 TB/s, for the automatic tile (128x128 with
+    128-byte K steps and split-K) and, for comparison, the weight-streaming tile."""
     import torch
 
     from d3trt_amd import _lib
@@ -738,7 +738,7 @@ def run_question_gemms(args):
         a_s = torch.rand(M, generator=gen, device=dev) * 1e-3
         y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
         res = {"M": M, "N": N, "K": Kd}
-        for label, tile in (("", _lib.TILE_AUTO), ("splitk_tile_", _lib.TILE_DMA_128_W4_K128)):
+        for label, tile in (("", _lib.TILE_AUTO), ("ws_tile_", _lib.TILE_WS)):
             us = launch_us(lambda i: K.gemm("fp8", a, a_s, ws[i % copies], w_s, out=y, tile=tile), 2 * copies)
             res[label + "us"] = round(us, 2)
             res[label + "frac_hbm"] = round(gemm_bytes(M, N, Kd) / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 3)
@@ -749,8 +749,8 @@ def run_question_gemms(args):
         del ws
         torch.cuda.empty_cache()
     out["note"] = ("graph replay of back-to-back launches (median of >= 20), weights rotated over > 600 MB; "
-                   "automatic tile = weight streaming (no split-K); splitk_tile_* = the 128x128 tile with "
-                   "128-byte K steps and its automatic split-K (partials + reduce launch)")
+                   "automatic tile = 128x128 with 128-byte K steps and split-K (partials + reduce launch); "
+                   "ws_tile_* = the weight-streaming tile (one launch, no split-K workspace)")
     return out
 
 
