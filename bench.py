@@ -719,8 +719,8 @@ def run_question_gemms(args):
     """The four projections at question-batch M = 128 (8 blocks x 16 tokens), FP8: HBM-bound weight
     streams. Back-to-back launches replayed from a HIP graph, each reading a different weight copy from a
     pool of > 600 MB, so no launch finds its weights in the 256 MB Infinity Cache; median of >= 20
-    replays. Weight GB/s and algorithmic GB/s against 8 TB/s, for the automatic tile (128x128 with
-    128-byte K steps and split-K) and, for comparison, the weight-streaming tile."""
+    replays. Weight GB/s and algorithmic GB/s against 8 TB/s, for the automatic tile and, for
+    comparison, the weight-streaming tile chosen explicitly."""
     import torch
 
     from d3trt_amd import _lib
@@ -749,8 +749,9 @@ def run_question_gemms(args):
         del ws
         torch.cuda.empty_cache()
     out["note"] = ("graph replay of back-to-back launches (median of >= 20), weights rotated over > 600 MB; "
-                   "automatic tile = 128x128 with 128-byte K steps and split-K (partials + reduce launch); "
-                   "ws_tile_* = the weight-streaming tile (one launch, no split-K workspace)")
+                   "automatic tile = the planner's choice at M <= 128: the weight-streaming tile where K <= 4096 "
+                   "and its slabs fit one round of CUs (qkv, o_proj), else 128x128 with 128-byte K steps and "
+                   "split-K (gate_up, down); ws_tile_* = the weight-streaming tile chosen explicitly")
     return out
 
 

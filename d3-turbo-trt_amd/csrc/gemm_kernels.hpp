@@ -549,7 +549,12 @@ __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F
 // cannot prove disjoint, draining the pipeline); every wait on this DMA is
 // explicit (wait_vmcnt + barrier). M0 holds the LDS address: it is an input
 // operand bound to m0 ("{m0}"), so the compiler writes m0 itself and knows
-// its value at every point; the s_nop covers the M0-write -> LDS-DMA hazard.
+// its value at every point. The compiler does not insert wait states for an
+// inline asm's operands, so the asm carries its own: s_nop 4 gives the 5 wait
+// states a VMEM instruction needs after a VALU write of an SGPR it reads (the
+// base comes from v_readfirstlane, often only an instruction or two earlier;
+// with fewer, the DMA can read the register's previous value), which also
+// covers the single wait state after an M0 write.
 // A wave-uniform pointer, pinned to SGPRs (the DMA asm takes it as an SGPR pair).
 __device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* q) {
   const uint64_t v = (uint64_t)(uintptr_t)q;
@@ -561,7 +566,7 @@ __device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* q) {
 template <int OFF>
 __device__ __forceinline__ void dma16(const uint8_t* gbase, uint32_t voff, uint32_t lds_base) {
   asm volatile(
-      "s_nop 0\n\t"
+      "s_nop 4\n\t"
       "global_load_lds_dwordx4 %0, %1"
       :
       : "v"(voff), "s"(gbase), "{m0}"(lds_base + (uint32_t)OFF)

@@ -1,70 +1,56 @@
-// Weight-streaming W8A8 GEMM for skinny M (question batches, M <= 128 tokens;
-// correct for any M): one launch, no split-K workspace.
+// Weight-streaming W8A8 GEMM for skinny M (question batches, M <= 128 tokens
+// per workgroup; any M by row parts): one launch, no split-K workspace, a
+// dedicated weight-streaming wave.
 //
-// A question batch runs every projection at small M, where the GEMM is a
-// stream of the weight matrix (N x K bytes) past a few activation rows that
-// stay in L2. What bounds it is how many weight bytes each CU keeps in flight
-// and how early a short-lived workgroup asks for them, not the MFMAs.
+// At M <= 128 the GEMM is a stream of the weight matrix (N x K bytes, HBM)
+// past a few activation rows (L2-resident). Two facts shape the kernel:
 //
-//   * A workgroup owns a slab of 32 * NB output columns (NB = 2 for the SwiGLU
-//     gate/up pairs) and MB blocks of 32 rows, over the whole of K. Its four
-//     waves split K: wave w takes the 128-byte K blocks w, w + 4, w + 8, ...
-//   * Weights: each wave DMAs its own K blocks of the slab into a private LDS
-//     ring (global_load_lds_dwordx4, 8 rows of 128 bytes per instruction:
-//     whole 128-byte lines of each weight row), RW blocks deep. No wave reads
-//     another wave's ring, so the K loop has no barrier.
-//   * Activations: each wave loads its K blocks of the MB x 32 rows straight
-//     into VGPRs (DA blocks deep); nothing is shared, so nothing goes through
-//     LDS.
-//   * K order inside a 128-byte block: lane (row r, half h) holds the 64
-//     contiguous bytes [64 h, 64 h + 64) of row r; MFMA a of the block takes
-//     its piece a (32 bytes for FP8 32x32x64, 16 for INT8 32x32x32). Both
-//     operands use the same assignment, so every product of the block is
-//     taken exactly once; the weight rows in LDS are read with the same
-//     64-byte split (XOR-swizzled 16-byte chunks, conflict-free).
-//   * Every wave ends with a partial sum of its K blocks. The partials meet in
-//     LDS and are added in wave order 0, 1, 2, 3 (INT8 exact; FP8 in a fixed
-//     fp32 order that depends on K only, so any M gives the same bits), then
-//     wave i runs the shared epilogue on M block i.
-//   * All memory operations of the K loop are inline asm with explicit
-//     vmcnt waits (in issue order: weights of block t + RW - 1, then
-//     activations of block t + DA - 1, then the wait for block t), so the
-//     compiler's own waits never cover a load that is not needed yet.
+//   * vmcnt counts a wave's memory operations in issue order, so a wave that
+//     loads both operands can only keep its weights as far ahead as its
+//     activations. Weights come from HBM (microseconds away under load) and
+//     activations from L2, so they need different lead. Here they are issued
+//     by different waves: one producer wave DMAs the weight slab into a deep
+//     LDS ring (DW blocks) and does nothing else; the consumer waves DMA
+//     their own activation rows into shallow private rings (DA blocks) and
+//     run the MFMAs. Each wave waits only on its own counter.
+//   * Whole 128-byte lines per request: every DMA instruction moves 8 rows x
+//     128 bytes (one K block of 8 rows) of either operand, so the vector
+//     memory path handles 8 lines per KiB.
+//
+// Layout. A workgroup owns a slab of 32 * NB output columns (NB = 2 for the
+// SwiGLU gate/up pairs) and MB blocks of 32 rows. Consumer c (of CW) owns
+// row blocks c * RB .. c * RB + RB - 1 (RB = MB / CW) and every column of the
+// slab: it reads every weight block (shared through the ring) and only its
+// own activation rows. K blocks are 128 bytes; inside a block the MFMA
+// operand chunks are assigned as in the pipelined tiles (FP8 sub-step s, lane
+// half h: 16-byte chunks 4 s + 2 h and 4 s + 2 h + 1; INT8: 2 s + h), and
+// blocks are summed in K order, so results equal the unsplit 128x128 tile with
+// 128-byte K steps bit for bit.
+//
+// Synchronization, per K block t: the producer waits for its DMA of weight
+// block t and joins barrier t; a consumer waits for its activation block t and
+// joins barrier t, then reads both operands. After barrier t every consumer
+// has finished block t - 1 (its LDS reads completed before it arrived), so the
+// producer refills that slot with block t + DW - 1. Activation slots are
+// private: a consumer refills the slot of block t - 1 at the start of
+// iteration t. Every wave passes the same nkb barriers; the producer then
+// leaves and each consumer runs the shared epilogue on its rows, staging
+// through its own activation ring.
+//
+// Cost (MI355X, M = 128, weights from HBM). Every workgroup reads all M x K
+// activation bytes from L2, and that stream runs at ~47 GB/s per CU, so the
+// kernel wins where M x K is small against the split-K alternative's partial
+// sums and second launch: QKV 128 x 6144 x 4096 13.5 us and o_proj
+// 128 x 4096 x 4096 13.0 us, against 17.6 and 16.5 us for the 128x128 tile
+// split over K; down (K = 12288) 34.5 against 21.8 us. Deeper weight or
+// activation rings and more producer waves measured no faster.
 #pragma once
 
 #include "gemm_kernels.hpp"
 
 namespace d3 {
 
-constexpr int kWsKB = 128;               // bytes of K per block
-constexpr int kWsWaveLds = 35 * 1024;    // LDS per wave for its weight ring (and later its partials)
-
-template <int MODE, int MB, int NB, int EPI, int OUT>
-struct WsCfg {
-  static constexpr int SUB = MODE == kInt8 ? 4 : 2;          // MFMAs along K per block
-  static constexpr int WBLK = NB * 32 * kWsKB;                // weight bytes per block (one wave)
-  static constexpr int WDMA = WBLK / 1024;                    // DMA instructions per block
-  static constexpr int ADMA = MB * 4;                         // 16-byte activation loads per lane per block
-  static constexpr int DA = MB <= 2 ? 4 : 3;                  // activation blocks in VGPRs
-  static constexpr int RING = kWsWaveLds / WBLK;              // weight blocks the LDS ring holds
-  // at most 63 memory operations may be outstanding (vmcnt is 6 bits)
-  static constexpr int RW_VM = (63 - (DA - 1) * ADMA) / WDMA + 1;
-  static constexpr int RW = RING < RW_VM ? RING : RW_VM;      // weight blocks in the ring
-  static constexpr int STEADY_WAIT = (DA - 1) * (WDMA + ADMA);
-  using E = EpiLds<NB, EPI, OUT>;
-  static constexpr int LDS = 4 * kWsWaveLds + 4 * E::BYTES;
-  static_assert(RW >= DA && DA >= 2, "ring depth");
-  static_assert(STEADY_WAIT <= 63, "vmcnt range");
-  static_assert(MB * NB * 4096 <= kWsWaveLds, "partials fit the wave's region");
-  static_assert(LDS <= 160 * 1024, "LDS");
-};
-
-// 16-byte global load into VGPRs, invisible to the compiler's wait insertion (explicit vmcnt waits).
-__device__ __forceinline__ uint4 ws_load16(const uint8_t* p) {
-  uint4 v;
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
-  return v;
-}
+constexpr int kWsKB = 128;  // bytes of K per block
 
 // s_waitcnt vmcnt(n) for a wave-uniform runtime n in [0, MAXN]
 template <int MAXN>
@@ -74,221 +60,191 @@ __device__ __forceinline__ void ws_wait_vm(int n) {
   });
 }
 
-template <int MODE, int MB, int NB, int EPI, int OUT>
-__global__ __launch_bounds__(256, 1) void gemm_w8a8_ws(GemmParams p) {
-  using C = WsCfg<MODE, MB, NB, EPI, OUT>;
+
+template <int MODE, int MB, int NB, int CW, int DW, int DA, int EPI, int OUT>
+struct WsCfg {
+  static_assert(MB % CW == 0, "row blocks split evenly over the consumers");
+  static constexpr int RB = MB / CW;                    // row blocks per consumer
+  static constexpr int SUB = MODE == kInt8 ? 4 : 2;     // MFMAs along K per block
+  static constexpr int WBLK = NB * 32 * kWsKB;           // weight bytes per block
+  static constexpr int WDMA = WBLK / 1024;               // producer DMA instructions per block
+  static constexpr int ABLK = RB * 32 * kWsKB;           // activation bytes per block per consumer
+  static constexpr int ADMA = ABLK / 1024;               // consumer DMA instructions per block
+  static constexpr int W_STEADY = (DW - 2) * WDMA;       // producer: blocks t+1 .. t+DW-2 may be in flight
+  static constexpr int A_STEADY = (DA - 1) * ADMA;       // consumer: blocks t+1 .. t+DA-1 may be in flight
+  static constexpr int W_BYTES = DW * WBLK;
+  static constexpr int A_BYTES = CW * DA * ABLK;
+  static constexpr int LDS = W_BYTES + A_BYTES;
+  using E = EpiLds<NB, EPI, OUT>;
+  static_assert(DW >= 2 && DA >= 2, "ring depth");
+  static_assert(W_STEADY <= 63 && A_STEADY <= 63, "vmcnt range");
+  static_assert(E::BYTES <= DA * ABLK, "epilogue staging fits the consumer's ring");
+  static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+template <int MODE, int MB, int NB, int CW, int DW, int DA, int EPI, int OUT>
+__global__ __launch_bounds__((CW + 1) * 64, 1) void gemm_w8a8_ws(GemmParams p) {
+  using C = WsCfg<MODE, MB, NB, CW, DW, DA, EPI, OUT>;
   using MF = Mfma<MODE>;
   typedef typename MF::frag frag_t;
   typedef typename MF::acc acc_t;
-  constexpr int SUB = C::SUB, DA = C::DA, RW = C::RW, WDMA = C::WDMA, ADMA = C::ADMA;
+  constexpr int RB = C::RB, SUB = C::SUB, WDMA = C::WDMA, ADMA = C::ADMA;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
 
   const int lane = threadIdx.x & 63, lrow = lane & 31, lhalf = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // workgroup -> (column slab, row part); the row parts of one slab run on the same XCD (ids 8 apart),
-  // so the second read of the slab's weights hits that XCD's L2
+  // workgroup -> (column slab, row part): consecutive slabs on one XCD
   const int bid = blockIdx.x, xcd = bid & 7, local = bid >> 3;
   const int part = local % p.tiles_m;
   const int slab = (local / p.tiles_m) * 8 + xcd;
-  if (slab >= p.tiles_n) return;
+  if (slab >= p.tiles_n) return;  // the whole workgroup leaves: no barrier is pending
   const int64_t n0 = (int64_t)slab * (32 * NB);
   const int64_t m0 = (int64_t)part * (32 * MB);
   const int nkb = (int)(p.K / kWsKB);
-  const int cnt = nkb > wave ? (nkb - wave + 3) / 4 : 0;  // this wave's K blocks: wave, wave + 4, ...
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)D3_LDS_PTR(lds));
 
-  // weight DMA: instruction d of a block covers slab rows 8 d .. 8 d + 7; lane j -> row 8 d + j / 8,
-  // physical chunk j % 8 = logical chunk (j % 8) ^ swz(row); rows past N repeat row N - 1 (never stored)
-  uint32_t w_off[WDMA];
+  if (wave == CW) {
+    // ---------------- producer: the weight slab, DW blocks deep ----------------
+    // instruction d covers slab rows 8 d .. 8 d + 7: lane j -> row 8 d + j / 8, LDS chunk j % 8 holds
+    // logical chunk (j % 8) ^ swz(row); rows past N repeat row N - 1 (their outputs are never stored)
+    uint32_t w_off[WDMA];
 #pragma unroll
-  for (int d = 0; d < WDMA; ++d) {
+    for (int d = 0; d < WDMA; ++d) {
+      const int row = 8 * d + (lane >> 3);
+      const int ch = (lane & 7) ^ lds_swz<kWsKB>(row);
+      w_off[d] = (uint32_t)((min(n0 + row, p.N - 1) - n0) * p.ldw + ch * 16);
+    }
+    const uint8_t* w_slab = p.w + n0 * p.ldw;
+    auto issue_w = [&](int t) {
+      const uint8_t* g = uniform_ptr(w_slab + (int64_t)t * kWsKB);
+      const uint32_t slot = lds0 + (uint32_t)(t % DW) * C::WBLK;
+      static_for<0, WDMA>([&](auto d_c) {
+        constexpr int d = decltype(d_c)::value;
+        dma16<d * 1024>(g, w_off[d], slot);
+      });
+    };
+    for (int t = 0; t < DW - 1 && t < nkb; ++t) issue_w(t);
+    for (int t = 0; t < nkb; ++t) {
+      // blocks issued so far: 0 .. min(nkb, t + DW - 1) - 1; all after block t may stay in flight
+      if (t + DW - 1 <= nkb) {
+        wait_vmcnt<C::W_STEADY>();
+      } else {
+        ws_wait_vm<C::W_STEADY>((nkb - t - 1) * WDMA);
+      }
+      lds_barrier();  // barrier t: block t is in LDS; every consumer is done with block t - 1
+      if (t + DW - 1 < nkb) issue_w(t + DW - 1);  // into the slot of block t - 1
+    }
+    return;
+  }
+
+  // ---------------- consumer c: row blocks c RB .. c RB + RB - 1 ----------------
+  const int c = wave;
+  const int64_t r0 = m0 + 32 * RB * c;  // first row of this consumer
+  uint32_t a_off[ADMA];
+#pragma unroll
+  for (int d = 0; d < ADMA; ++d) {
     const int row = 8 * d + (lane >> 3);
     const int ch = (lane & 7) ^ lds_swz<kWsKB>(row);
-    w_off[d] = (uint32_t)((min(n0 + row, p.N - 1) - n0) * p.ldw + ch * 16);
+    a_off[d] = (uint32_t)((min(r0 + row, p.M - 1) - r0) * p.lda + ch * 16);
   }
-  const uint8_t* w_slab = p.w + n0 * p.ldw;
-  const uint32_t ring0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)D3_LDS_PTR(lds) +
-                                                        (uint32_t)wave * (uint32_t)kWsWaveLds);
-  // activations: lane (r, h) of M block i reads row m0 + 32 i + r (clamped), bytes [64 h, 64 h + 64)
-  const uint8_t* a_row[MB];
+  // rows past M read row M - 1; if this consumer's first row is past M it still runs the loop (the
+  // barriers are shared) on clamped rows and stores nothing
+  const uint8_t* a_rows = p.a + min(r0, p.M - 1) * p.lda;
+  if (r0 >= p.M) {
 #pragma unroll
-  for (int i = 0; i < MB; ++i) a_row[i] = p.a + min(m0 + 32 * i + lrow, p.M - 1) * p.lda + 64 * lhalf;
-
-  auto issue_w = [&](int t) {  // weights of this wave's block t into ring slot t % RW
-    const int kb = wave + 4 * t;
-    const uint8_t* g = uniform_ptr(w_slab + (int64_t)kb * kWsKB);
-    const uint32_t slot = ring0 + (uint32_t)(t % RW) * C::WBLK;
-    static_for<0, WDMA>([&](auto d_c) {
+    for (int d = 0; d < ADMA; ++d) a_off[d] = (uint32_t)((lane & 7) ^ lds_swz<kWsKB>(8 * d + (lane >> 3))) * 16;
+  }
+  const uint32_t aring = lds0 + (uint32_t)C::W_BYTES + (uint32_t)c * (uint32_t)(DA * C::ABLK);
+  auto issue_a = [&](int t) {
+    const uint8_t* g = uniform_ptr(a_rows + (int64_t)t * kWsKB);
+    const uint32_t slot = aring + (uint32_t)(t % DA) * C::ABLK;
+    static_for<0, ADMA>([&](auto d_c) {
       constexpr int d = decltype(d_c)::value;
-      dma16<d * 1024>(g, w_off[d], slot);
+      dma16<d * 1024>(g, a_off[d], slot);
     });
   };
-  uint4 ra[DA][MB][4];
-  auto issue_a = [&](auto s_c, int t) {  // activations of block t into register slot s
-    constexpr int s = decltype(s_c)::value;
-    const int64_t kb = wave + 4 * t;
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) ra[s][i][c] = ws_load16(a_row[i] + kb * kWsKB + 16 * c);
-  };
 
-  acc_t acc[MB][NB];
+  acc_t acc[RB][NB];
 #pragma unroll
-  for (int i = 0; i < MB; ++i)
+  for (int i = 0; i < RB; ++i)
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  // prologue: the issue pattern of iterations -(RW - 1) .. -1 (weights of blocks 0 .. RW - 2, with the
-  // activations of blocks 0 .. DA - 2 after the weights of the iterations they belong to)
-  static_for<0, RW - 1>([&](auto v_c) {
-    constexpr int v = decltype(v_c)::value;  // iteration v - (RW - 1)
-    if (v < cnt) issue_w(v);
-    constexpr int ab = v - (RW - 1) + DA - 1;  // activation block of that iteration
-    if constexpr (ab >= 0) {
-      if (ab < cnt) issue_a(std::integral_constant<int, ab % DA>{}, ab);
-    }
-  });
-
-  // one block: iteration t with activations in register slot s = t % DA
-  auto block = [&](auto s_c, int t) {
-    constexpr int s = decltype(s_c)::value;
-    if (t + RW - 1 < cnt) issue_w(t + RW - 1);
-    if (t + DA - 1 < cnt) issue_a(std::integral_constant<int, (s + DA - 1) % DA>{}, t + DA - 1);
-    // wait for block t: every operation issued after its activation loads may stay outstanding
-    if (t + RW - 1 < cnt) {
-      wait_vmcnt<C::STEADY_WAIT>();
+  for (int t = 0; t < DA - 1 && t < nkb; ++t) issue_a(t);
+  const uint8_t* a_lds = lds + C::W_BYTES + (size_t)c * (DA * C::ABLK);
+  for (int t = 0; t < nkb; ++t) {
+    if (t + DA - 1 < nkb) issue_a(t + DA - 1);  // into the slot of block t - 1 (read last iteration)
+    // blocks issued so far: 0 .. min(nkb, t + DA) - 1; all after block t may stay in flight
+    if (t + DA <= nkb) {
+      wait_vmcnt<C::A_STEADY>();
     } else {
-      int n = 0;
-#pragma unroll
-      for (int u = 1; u < DA; ++u) {  // iterations t - DA + 1 + u, the ones after block t's loads were issued
-        const int it = t - DA + 1 + u;
-        n += (it + RW - 1 < cnt ? WDMA : 0) + (it + DA - 1 < cnt ? ADMA : 0);
-      }
-      ws_wait_vm<C::STEADY_WAIT>(n);
+      ws_wait_vm<C::A_STEADY>((nkb - t - 1) * ADMA);
     }
-    asm volatile("" ::: "memory");  // the ring was written by DMA the compiler does not see
+    lds_barrier();  // barrier t: the producer's weight block t is in LDS as well
     __builtin_amdgcn_sched_barrier(0);
-    // weight fragments of block t from the ring: lane (r, h) of N block j, MFMA a reads its row's logical
-    // chunks (SUB == 2: 4 h + 2 a, 4 h + 2 a + 1; SUB == 4: 4 h + a)
-    const uint8_t* slot = lds + (size_t)wave * kWsWaveLds + (size_t)(t % RW) * C::WBLK;
-    frag_t wf[NB][SUB];
+    const uint8_t* ws = lds + (size_t)(t % DW) * C::WBLK;
+    const uint8_t* as = a_lds + (size_t)(t % DA) * C::ABLK;
+    frag_t wf[SUB][NB], af[SUB][RB];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const int row = 32 * j + lrow;
+    for (int s = 0; s < SUB; ++s) {
 #pragma unroll
-      for (int a = 0; a < SUB; ++a) {
+      for (int j = 0; j < NB; ++j) {
+        const int row = 32 * j + lrow;
         if constexpr (MODE == kInt8) {
-          wf[j][a] = *(const v4i*)(slot + lds_offk<kWsKB>(row, 4 * lhalf + a));
+          wf[s][j] = *(const v4i*)(ws + lds_offk<kWsKB>(row, 2 * s + lhalf));
         } else {
-          const v4i lo = *(const v4i*)(slot + lds_offk<kWsKB>(row, 4 * lhalf + 2 * a));
-          const v4i hi = *(const v4i*)(slot + lds_offk<kWsKB>(row, 4 * lhalf + 2 * a + 1));
-          wf[j][a] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          const v4i lo = *(const v4i*)(ws + lds_offk<kWsKB>(row, 4 * s + 2 * lhalf));
+          const v4i hi = *(const v4i*)(ws + lds_offk<kWsKB>(row, 4 * s + 2 * lhalf + 1));
+          wf[s][j] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int row = 32 * i + lrow;
+        if constexpr (MODE == kInt8) {
+          af[s][i] = *(const v4i*)(as + lds_offk<kWsKB>(row, 2 * s + lhalf));
+        } else {
+          const v4i lo = *(const v4i*)(as + lds_offk<kWsKB>(row, 4 * s + 2 * lhalf));
+          const v4i hi = *(const v4i*)(as + lds_offk<kWsKB>(row, 4 * s + 2 * lhalf + 1));
+          af[s][i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
       }
     }
-    __builtin_amdgcn_sched_barrier(0);  // every weight read of the block ahead of its MFMAs: one LDS latency
 #pragma unroll
-    for (int a = 0; a < SUB; ++a)
+    for (int s = 0; s < SUB; ++s)
 #pragma unroll
-      for (int i = 0; i < MB; ++i) {
-        frag_t af;
-        if constexpr (MODE == kInt8) {
-          const uint4 v = ra[s][i][a];
-          af = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-        } else {
-          const uint4 lo = ra[s][i][2 * a], hi = ra[s][i][2 * a + 1];
-          af = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
+      for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int j = 0; j < NB; ++j) acc[i][j] = MF::run(wf[j][a], af, acc[i][j]);
-      }
-    // this slot's LDS reads are done before a later DMA refills it
-    wait_lgkm0();
+        for (int j = 0; j < NB; ++j) acc[i][j] = MF::run(wf[s][j], af[s][i], acc[i][j]);
+    wait_lgkm0();  // this block's LDS reads are done before its slots are refilled
     __builtin_amdgcn_sched_barrier(0);
-  };
-  for (int t0 = 0; t0 < cnt; t0 += DA) {
-    static_for<0, DA>([&](auto s_c) {
-      if (t0 + decltype(s_c)::value < cnt) block(s_c, t0 + decltype(s_c)::value);
-    });
   }
-
-  // partials -> this wave's region: 16-byte word (i, j, g) of lane l at ((i NB + j) 4 + g) 64 + l
-  uint4* mine = (uint4*)(lds + (size_t)wave * kWsWaveLds);
-#pragma unroll
-  for (int i = 0; i < MB; ++i)
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        using EL = typename std::conditional<MODE == kInt8, int, float>::type;
-        mine[((i * NB + j) * 4 + g) * 64 + lane] =
-            make_uint4(__builtin_bit_cast(uint32_t, (EL)acc[i][j][4 * g]), __builtin_bit_cast(uint32_t, (EL)acc[i][j][4 * g + 1]),
-                       __builtin_bit_cast(uint32_t, (EL)acc[i][j][4 * g + 2]), __builtin_bit_cast(uint32_t, (EL)acc[i][j][4 * g + 3]));
-      }
-  __syncthreads();
-  if (wave >= MB) return;
-  // wave i: M block i, the four partials added in wave order
-  acc_t sum[1][NB];
-#pragma unroll
-  for (int j = 0; j < NB; ++j)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sum[0][j][r] = 0;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const uint4* part_u = (const uint4*)(lds + (size_t)u * kWsWaveLds);
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        using EL = typename std::conditional<MODE == kInt8, int, float>::type;
-        const uint4 v = part_u[((wave * NB + j) * 4 + g) * 64 + lane];
-        sum[0][j][4 * g] = (EL)sum[0][j][4 * g] + __builtin_bit_cast(EL, v.x);
-        sum[0][j][4 * g + 1] = (EL)sum[0][j][4 * g + 1] + __builtin_bit_cast(EL, v.y);
-        sum[0][j][4 * g + 2] = (EL)sum[0][j][4 * g + 2] + __builtin_bit_cast(EL, v.z);
-        sum[0][j][4 * g + 3] = (EL)sum[0][j][4 * g + 3] + __builtin_bit_cast(EL, v.w);
-      }
-  }
-  epilogue<MODE, 1, NB, EPI, OUT>(p, sum, m0 + 32 * wave, n0, lane, lds + 4 * kWsWaveLds + wave * C::E::BYTES);
+  if (r0 >= p.M) return;
+  // the last activation slots were read (wait_lgkm0 above) and no DMA targets them any more
+  epilogue<MODE, RB, NB, EPI, OUT>(p, acc, r0, n0, lane, (uint8_t*)a_lds);
 }
 
-// Host side: MB row blocks per workgroup, p.tiles_m row parts, p.tiles_n column slabs.
+// Host side: MB row blocks per workgroup (p.tiles_m row parts), p.tiles_n column slabs. One consumer
+// per row block; the weight ring 8 blocks deep (NB = 2 keeps its vmcnt lead within 63), activations 3.
 template <int MODE, int EPI, int OUT, int MB>
 static hipError_t launch_ws_mb(GemmParams p, hipStream_t st) {
   constexpr int NB = EPI == kEpiSwiGLU ? 2 : 1;
+  constexpr int CW = MB, DW = 8, DA = 3;
   const int64_t slabs8 = ((int64_t)p.tiles_n + 7) / 8 * 8;
-  hipLaunchKernelGGL((gemm_w8a8_ws<MODE, MB, NB, EPI, OUT>), dim3((unsigned)(slabs8 * p.tiles_m)), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((gemm_w8a8_ws<MODE, MB, NB, CW, DW, DA, EPI, OUT>), dim3((unsigned)(slabs8 * p.tiles_m)),
+                     dim3((CW + 1) * 64), 0, st, p);
   return hipGetLastError();
-}
-
-// Row blocks per part (1-4) and row parts for M rows and `slabs` column slabs: the split with the
-// fewest bytes per CU (each workgroup reads its rows' activations and its slab's weights over all of
-// K; workgroups beyond one per CU run in further rounds).
-inline void ws_partition(int64_t M, int64_t slabs, int nb, int64_t cus, int& mb, int& parts) {
-  const int64_t mblocks = (M + 31) / 32;
-  int64_t best = -1;
-  mb = 4;
-  parts = (int)((mblocks + 3) / 4);
-  for (int p = (int)((mblocks + 3) / 4); p <= mblocks && p <= 4 * ((mblocks + 3) / 4); p *= 2) {
-    const int64_t b = (mblocks + p - 1) / p;
-    const int64_t rounds = (slabs * p + cus - 1) / cus;
-    const int64_t cost = rounds * (b + nb);
-    if (best < 0 || cost < best) {
-      best = cost;
-      mb = (int)b;
-      parts = p;
-    }
-  }
 }
 
 template <int MODE, int EPI, int OUT>
 static hipError_t launch_ws(GemmParams p, hipStream_t st) {
   if (p.ksplit != 1) return hipErrorInvalidValue;
   constexpr int NB = EPI == kEpiSwiGLU ? 2 : 1;
-  int mb, parts;
-  ws_partition(p.M, (p.N + 32 * NB - 1) / (32 * NB), NB, device_cu_count(), mb, parts);
-  p.tiles_m = parts;
+  const int64_t mblocks = (p.M + 31) / 32;
+  const int mb = (int)std::min<int64_t>(mblocks, 4);
+  p.tiles_m = (int)((mblocks + mb - 1) / mb);
   p.tiles_n = (int)((p.N + 32 * NB - 1) / (32 * NB));
   switch (mb) {
     case 1: return launch_ws_mb<MODE, EPI, OUT, 1>(p, st);

@@ -62,8 +62,9 @@ extern "C" {
 #define D3W8A8_TILE_DMA_256x192_W4 8 /* DMA 256x192, 4 waves: whole tile rounds where 256x256 leaves one ragged
                                       * (fused QKV, N = 6144); not with D3W8A8_EPI_SWIGLU */
 #define D3W8A8_TILE_WS 9             /* weight streaming for skinny M (question batches): 32-column slabs
-                                      * (64 with SwiGLU), the four waves split K, no split-K workspace;
-                                      * K % 128 == 0; FP8 rows do not depend on M */
+                                      * (64 with SwiGLU), one wave streams the weights, one per 32 rows
+                                      * computes; no split-K workspace; K % 128 == 0; results equal
+                                      * tile 7 unsplit bit for bit (so FP8 rows do not depend on M) */
 
 const char* d3w8a8_version(void);
 const char* d3w8a8_last_error(void);

@@ -144,8 +144,16 @@ def test_split_k_plan_on_the_host():
     # the weight-streaming tile never splits K
     assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, _lib.TILE_WS, -1, big) == 0
     assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, _lib.TILE_WS, 2, big) == -1
-    # the automatic tile at question-batch M is the 128x128 one with 128-byte steps, split as below
-    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, big) == 32 * 4 * slot
+    # the automatic tile at question-batch M (any M <= 128 alike): weight streaming where K <= 4096
+    # and its slabs fit one round of CUs (o_proj, QKV), else the 128x128 tile with 128-byte steps,
+    # split as below (down, K = 12288); 768 slabs of 32 columns exceed a round, and their 192 tiles
+    # of 128x128 fill the GPU unsplit
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, big) == 0
+    assert lib.d3w8a8_gemm_workspace(128, 6144, 4096, 4096, 4096, -1, -1, big) == 0
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 12288, 12288, 12288, -1, -1, big) == 32 * 8 * slot
+    assert lib.d3w8a8_gemm_workspace(128, 24576, 4096, 4096, 4096, -1, -1, big) == 0
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, 0) == 0
+    assert lib.d3w8a8_gemm_workspace(16, 4096, 12288, 12288, 12288, -1, -1, big) == 32 * 8 * slot
     # on the 128x128 tile, 128 rows x 4096 columns: 32 tiles leave the GPU idle -> 4 splits of 1 KiB of K
     assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, k128, -1, big) == 32 * 4 * slot
     # down projection (K = 12288): 8 splits make ~one workgroup per CU

@@ -1,9 +1,10 @@
 """GPU parity of the weight-streaming tile (skinny M, the question batches' GEMMs).
 
-Its waves split K into 128-byte blocks and add their partial sums in a fixed order that depends on K
-only: INT8 accumulators are exact for every shape, and FP8 rows come out bit-identical whatever M
-is (a row computed alone equals the same row inside a 128-row batch), which is what lets a packed
-question batch equal its blocks run one by one.
+One wave streams the weight slab, one wave per 32 rows computes, and the K blocks are summed in K
+order with the same MFMA operand assignment as the 128x128 tile with 128-byte K steps: every result
+equals that tile's unsplit result bit for bit (INT8 and FP8, every epilogue), so FP8 rows come out
+identical whatever M is (a row computed alone equals the same row inside a 128-row batch), which is
+what lets a packed question batch equal its blocks run one by one.
 """
 
 from __future__ import annotations
@@ -104,6 +105,44 @@ def test_ws_ragged_row_map(dev, mode):
             qb, sb = K.quantize_rows(xd[b, :n], mode)
             assert torch.equal(out[b, :n], K.gemm(mode, qb, sb.view(-1), wd, wsd, tile=WS).cpu())
         assert torch.all(out[b, n:] == 0)
+
+
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
+@pytest.mark.parametrize("M", [1, 7, 32, 45, 96, 128, 160, 300])
+@pytest.mark.parametrize("N,Kd", [(64, 128), (100, 384), (640, 1024), (6144, 4096), (96, 12288)])
+def test_ws_equals_the_unsplit_128_tile(dev, mode, M, N, Kd):
+    """Dequant and residual epilogues: bit-equal to tile 7 without split-K (edge rows and columns
+    included, M over 128 as several row parts)."""
+    g = gen(M * 7 + N + Kd + (mode == "fp8"))
+    mk = rand_i8 if mode == "int8" else rand_fp8
+    a, w = mk(g, M, Kd).to(dev), mk(g, N, Kd).to(dev)
+    sa = torch.rand(M, generator=g).mul(1e-2).to(dev)
+    sw = torch.rand(N, generator=g).mul(1e-2).to(dev)
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16).to(dev)
+    k7 = _lib.TILE_DMA_128_W4_K128
+    for kw in (dict(), dict(epilogue=_lib.EPI_RESIDUAL, residual=res)):
+        got = K.gemm(mode, a, sa, w, sw, tile=WS, **kw)
+        want = K.gemm(mode, a, sa, w, sw, tile=k7, ksplit=1, **kw)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), kw.get("epilogue", "dequant")
+
+
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
+@pytest.mark.parametrize("M", [16, 33, 128])
+def test_ws_swiglu_equals_the_unsplit_128_tile(dev, mode, M):
+    g = gen(M + 5 * (mode == "fp8"))
+    H, I = 2048, 1536
+    mk = rand_i8 if mode == "int8" else rand_fp8
+    a, w = mk(g, M, H).to(dev), mk(g, 2 * I, H).to(dev)
+    sa = torch.rand(M, generator=g).mul(1e-2).to(dev)
+    sw = torch.rand(2 * I, generator=g).mul(1e-2).to(dev)
+    outs = []
+    for tile, ks in ((WS, _lib.KSPLIT_AUTO), (_lib.TILE_DMA_128_W4_K128, 1)):
+        amax = torch.zeros(M, device=dev)
+        h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+        K.gemm(mode, a, sa, w, sw, epilogue=_lib.EPI_SWIGLU, out=h, row_amax=amax, tile=tile, ksplit=ks)
+        outs.append((h, amax))
+    assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
+    assert torch.equal(outs[0][1], outs[1][1])
 
 
 def test_ws_never_splits_k(dev):
