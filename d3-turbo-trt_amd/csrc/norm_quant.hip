@@ -274,7 +274,8 @@ hipError_t launch_rmsnorm_quant_t(const void* x, int64_t ldx, const void* w, int
   if (M == 0) return hipSuccess;
   const size_t lds = (size_t)K * sizeof(float);  // the staged gain (K <= kMaxVecK: at most 64 KiB)
 #define L(N, F)                                                                                               \
-  hipLaunchKernelGGL((rmsnorm_quant_vec<MODE, DT, DTW, N, F>), row_grid(rmsnorm_quant_vec<MODE, DT, DTW, N, F>, M, lds), \
+  hipLaunchKernelGGL((rmsnorm_quant_vec<MODE, DT, DTW, N, F>),                                                 \
+                     row_grid(rmsnorm_quant_vec<MODE, DT, DTW, N, F>, M, lds, kNormRowBlocksPerCU),             \
                      dim3(256), lds, st, x, ldx, w, M, K, eps, zc, q, ldq, scale, normed, ldn, clear_amax)
   D3_NCH_DISPATCH(K, L);
 #undef L

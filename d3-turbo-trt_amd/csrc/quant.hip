@@ -34,13 +34,13 @@ int kernel_blocks_per_cu(const void* kernel, size_t lds_bytes) {
   return n;
 }
 
-int row_blocks_per_cu() {
+int row_blocks_per_cu(int dflt) {
   static const int v = [] {
     const char* e = getenv("D3W8A8_ROW_BLOCKS_PER_CU");
     const int n = e ? atoi(e) : 0;
-    return n >= 1 && n <= 1024 ? n : kRowBlocksPerCU;
+    return n >= 1 && n <= 1024 ? n : 0;
   }();
-  return v;
+  return v ? v : dflt;
 }
 
 int device_cu_count() {

@@ -240,18 +240,23 @@ inline dim3 quant_grid(int64_t rows) { return dim3((unsigned)((rows + kQuantWave
 // at most kRowBlocksPerCU per CU), so each wave walks several rows and
 // overlaps one row's loads with the previous row's arithmetic.
 constexpr int kRowBlocksPerCU = 1;  // 4 waves per CU, 1 per SIMD (measured best: the pipeline hides the rest)
-// kRowBlocksPerCU, or D3W8A8_ROW_BLOCKS_PER_CU from the environment (a tuning
-// override, read once; a large value gives every wave a single row).
-int row_blocks_per_cu();
+// The fused RMSNorm + quantize does more arithmetic per element (~13 VALU ops against ~5), so one
+// wave per SIMD leaves its loads and its arithmetic in series: every wave takes one row and the
+// occupancy sets the blocks per CU (4096 x 4096 INT8: 13.2 -> 12.0 us; 8192 x 4096: 22.2 -> 21.0).
+constexpr int kNormRowBlocksPerCU = 1024;
+// `dflt`, or D3W8A8_ROW_BLOCKS_PER_CU from the environment (a tuning
+// override for every row-pipelined kernel, read once; a large value gives
+// every wave a single row).
+int row_blocks_per_cu(int dflt);
 int device_cu_count();
 // Blocks of `kernel` (256 threads, lds_bytes of dynamic LDS) one CU holds at
 // once, cached per kernel.
 int kernel_blocks_per_cu(const void* kernel, size_t lds_bytes);
 template <typename K>
-inline dim3 row_grid(K kernel, int64_t rows, size_t lds_bytes) {
+inline dim3 row_grid(K kernel, int64_t rows, size_t lds_bytes, int per_cu_default = kRowBlocksPerCU) {
   const int occ = kernel_blocks_per_cu((const void*)kernel, lds_bytes);
   const int64_t need = (rows + kQuantWaves - 1) / kQuantWaves;
-  const int per_cu = row_blocks_per_cu();
+  const int per_cu = row_blocks_per_cu(per_cu_default);
   const int64_t cap = (int64_t)device_cu_count() * (occ < per_cu ? occ : per_cu);
   return dim3((unsigned)(need < cap ? need : cap));
 }
