@@ -104,12 +104,13 @@ int64_t rounds(int64_t tiles, int64_t cus) { return (tiles + cus - 1) / cus; }
 // 256-row tile would compute half its rows for nothing) streams the weights. When K % 128 == 0,
 // the weight-streaming kernel (gemm_ws.hpp, tile kWs) runs where K <= 4096 (each of its workgroups
 // reads M x K <= 512 KiB of activations) and its column slabs fit one round of CUs: no split-K
-// partials and no second launch (M = 128: QKV 13.5 vs 17.6 us, o_proj 13.0 vs 16.5 us). The rule
+// partials and no second launch (M = 128: QKV 13.5 vs 17.6 us, o_proj 13.0 vs 16.5 us, gate_up +
+// SwiGLU in 128-column slabs 28.9 vs 30.8 us). The rule
 // does not look at M, so every M <= 128 takes the same tile and split (a packed question batch
 // equals its blocks run one by one, FP8 included). Otherwise the
-// 128x128 tile with 128-byte K steps, split over K by the planner (down, K = 12288: 21.8 vs 34.5 us;
-// gate_up+SwiGLU: 384 slabs of 64 columns). Tile counts are weighed against the device's compute
-// units (`cus`; the thresholds were measured on 256).
+// 128x128 tile with 128-byte K steps, split over K by the planner (down, K = 12288: 21.8 vs 34.5 us).
+// Tile counts are weighed against the device's compute units (`cus`; the thresholds were measured on
+// 256).
 int choose_tile(int64_t M, int64_t N, int64_t K, bool fit, int epi, int64_t cus) {
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
@@ -117,8 +118,8 @@ int choose_tile(int64_t M, int64_t N, int64_t K, bool fit, int epi, int64_t cus)
   if (K % 64 == 0 && fit) {
     if (M <= 128) {
       if (K % 128 != 0) return kDma128w4;
-      const int64_t slabs = (N + (epi == kEpiSwiGLU ? 63 : 31)) / (epi == kEpiSwiGLU ? 64 : 32);
-      return K <= 4096 && slabs <= cus ? kWs : kDma128w4k128;
+      const int64_t cols = 32 * ws_slab_blocks(N, epi, cus);
+      return K <= 4096 && (N + cols - 1) / cols <= cus ? kWs : kDma128w4k128;
     }
     if (4 * t256 >= 3 * cus) {  // 192 tiles on 256 CUs
       if (epi != kEpiSwiGLU && N % 192 == 0) {

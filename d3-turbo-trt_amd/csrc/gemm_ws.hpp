@@ -226,31 +226,40 @@ __global__ __launch_bounds__((CW + 1) * 64, 1) void gemm_w8a8_ws(GemmParams p) {
   epilogue<MODE, RB, NB, EPI, OUT>(p, acc, r0, n0, lane, (uint8_t*)a_lds);
 }
 
-// Host side: MB row blocks per workgroup (p.tiles_m row parts), p.tiles_n column slabs. One consumer
-// per row block; the weight ring 8 blocks deep (NB = 2 keeps its vmcnt lead within 63), activations 3.
-template <int MODE, int EPI, int OUT, int MB>
+// Host side: MB row blocks per workgroup (p.tiles_m row parts), p.tiles_n column slabs of 32 NB columns.
+// One consumer per row block; activations 3 blocks deep; the weight ring 8 blocks deep (5 for NB = 4,
+// whose 16 DMAs per block would otherwise pass vmcnt's 63 and LDS).
+template <int MODE, int EPI, int OUT, int MB, int NB>
 static hipError_t launch_ws_mb(GemmParams p, hipStream_t st) {
-  constexpr int NB = EPI == kEpiSwiGLU ? 2 : 1;
-  constexpr int CW = MB, DW = 8, DA = 3;
+  constexpr int CW = MB, DW = NB == 4 ? 5 : 8, DA = 3;
   const int64_t slabs8 = ((int64_t)p.tiles_n + 7) / 8 * 8;
   hipLaunchKernelGGL((gemm_w8a8_ws<MODE, MB, NB, CW, DW, DA, EPI, OUT>), dim3((unsigned)(slabs8 * p.tiles_m)),
                      dim3((CW + 1) * 64), 0, st, p);
   return hipGetLastError();
 }
 
-template <int MODE, int EPI, int OUT>
-static hipError_t launch_ws(GemmParams p, hipStream_t st) {
-  if (p.ksplit != 1) return hipErrorInvalidValue;
-  constexpr int NB = EPI == kEpiSwiGLU ? 2 : 1;
+template <int MODE, int EPI, int OUT, int NB>
+static hipError_t launch_ws_nb(GemmParams p, hipStream_t st) {
   const int64_t mblocks = (p.M + 31) / 32;
   const int mb = (int)std::min<int64_t>(mblocks, 4);
   p.tiles_m = (int)((mblocks + mb - 1) / mb);
   p.tiles_n = (int)((p.N + 32 * NB - 1) / (32 * NB));
   switch (mb) {
-    case 1: return launch_ws_mb<MODE, EPI, OUT, 1>(p, st);
-    case 2: return launch_ws_mb<MODE, EPI, OUT, 2>(p, st);
-    case 3: return launch_ws_mb<MODE, EPI, OUT, 3>(p, st);
-    default: return launch_ws_mb<MODE, EPI, OUT, 4>(p, st);
+    case 1: return launch_ws_mb<MODE, EPI, OUT, 1, NB>(p, st);
+    case 2: return launch_ws_mb<MODE, EPI, OUT, 2, NB>(p, st);
+    case 3: return launch_ws_mb<MODE, EPI, OUT, 3, NB>(p, st);
+    default: return launch_ws_mb<MODE, EPI, OUT, 4, NB>(p, st);
+  }
+}
+
+template <int MODE, int EPI, int OUT>
+static hipError_t launch_ws(GemmParams p, hipStream_t st) {
+  if (p.ksplit != 1) return hipErrorInvalidValue;
+  if constexpr (EPI == kEpiSwiGLU) {
+    if (ws_slab_blocks(p.N, EPI, device_cu_count()) == 4) return launch_ws_nb<MODE, EPI, OUT, 4>(p, st);
+    return launch_ws_nb<MODE, EPI, OUT, 2>(p, st);
+  } else {
+    return launch_ws_nb<MODE, EPI, OUT, 1>(p, st);
   }
 }
 

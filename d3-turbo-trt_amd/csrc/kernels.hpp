@@ -97,4 +97,12 @@ int device_cu_count();
 // the environment (read once; a measurement switch).
 bool gemm_persistent();
 
+// Column slab of the weight-streaming tile: 32 columns, 64 (one gate/up pair) with SwiGLU, and two
+// pairs where 64-column slabs would not fit one round of CUs (gate_up, N = 24576 at M = 128: 28.9
+// against 35.5 us for 384 slabs of 64, and 30.8 us for the 128x128 tile).
+inline int ws_slab_blocks(int64_t N, int epi, int64_t cus) {
+  if (epi != kEpiSwiGLU) return 1;
+  return (N + 63) / 64 <= cus ? 2 : 4;
+}
+
 }  // namespace d3
