@@ -745,13 +745,23 @@ def run_question_gemms(args):
             if not label:
                 res["weight_gbs"] = round(N * Kd / (us * 1e-6) / 1e9, 1)
                 res["algo_gbs"] = round(gemm_bytes(M, N, Kd) / (us * 1e-6) / 1e9, 1)
+        if name == "gate_up":  # as the layer runs it: SwiGLU epilogue, half-width output, row amax
+            h = torch.empty(M, N // 2, dtype=torch.bfloat16, device=dev)
+            amax = torch.zeros(M, device=dev)
+            us = launch_us(lambda i: K.gemm("fp8", a, a_s, ws[i % copies], w_s, epilogue=_lib.EPI_SWIGLU, out=h,
+                                             row_amax=amax), 2 * copies)
+            sw_bytes = M * Kd + N * Kd + M * N + 4 * (2 * M + N)
+            res["swiglu_us"] = round(us, 2)
+            res["swiglu_frac_hbm"] = round(sw_bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 3)
         out[name] = res
         del ws
         torch.cuda.empty_cache()
     out["note"] = ("graph replay of back-to-back launches (median of >= 20), weights rotated over > 600 MB; "
                    "automatic tile = the planner's choice at M <= 128: the weight-streaming tile where K <= 4096 "
-                   "and its slabs fit one round of CUs (qkv, o_proj), else 128x128 with 128-byte K steps and "
-                   "split-K (gate_up, down); ws_tile_* = the weight-streaming tile chosen explicitly")
+                   "and its slabs fit one round of CUs (qkv, o_proj, gate_up with SwiGLU), else 128x128 with "
+                   "128-byte K steps and split-K (down; gate_up with a plain dequant epilogue); ws_tile_* = the "
+                   "weight-streaming tile chosen explicitly; gate_up swiglu_* = the layer's own gate_up launch "
+                   "(SwiGLU epilogue, half-width output, row amax)")
     return out
 
 

@@ -108,30 +108,42 @@ __global__ __launch_bounds__(256) void quant_rows_generic(const void* __restrict
 
 // ---------------------------------------------------------------------------
 // Requantization with a known row amax (SwiGLU output h [M, K]).
+// The scale comes from outside, so nothing waits for a whole row: the kernel
+// is a plain stream. One 256-thread block per row; thread t takes the
+// 8-element chunks t, t + 256, ... (NCT of them, K <= 2048 NCT), issues all
+// its loads (a chunk past the row's end re-reads the row's last chunk and is
+// not stored), forms the row scale while they fly, then quantizes and stores
+// 8 bytes per chunk. Many small blocks per CU keep the HBM queue full
+// (4096 x 12288 bf16: 31.0 us in the row-pipelined form, one wave per row).
 // ---------------------------------------------------------------------------
-template <int MODE, int DT, int NCH, bool FULL>
-__global__ __launch_bounds__(256) void quant_rows_amax_vec(const void* __restrict__ h, int64_t ldh,
-                                                          const float* __restrict__ amax_in, int64_t M,
-                                                          int64_t K, void* __restrict__ q, int64_t ldq,
-                                                          float* __restrict__ scale) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row0 = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
-  if (row0 >= M) return;
-  using RC = RowChunks<DT, NCH, FULL>;
-  pipeline_rows<RC>((const char*)h, ldh * RC::kES, row0, (int64_t)gridDim.x * kQuantWaves, M, K, lane, [] {},
-                    [&](RC& h_, int64_t row) {
-                      const RowScale s = scale_from_amax<MODE>(amax_in[row]);
-                      char* qr = (char*)q + row * ldq;
+template <int MODE, int DT, int NCT>
+__global__ __launch_bounds__(256) void quant_rows_amax_stream(const void* __restrict__ h, int64_t ldh,
+                                                             const float* __restrict__ amax_in, int64_t K,
+                                                             void* __restrict__ q, int64_t ldq,
+                                                             float* __restrict__ scale) {
+  using RC = RowChunks<DT, 1, true>;
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x;
+  const int64_t nch = K / 8;
+  const char* hr = (const char*)h + row * ldh * RC::kES;
+  RC v[NCT];
 #pragma unroll
-                      for (int c = 0; c < NCH; ++c) {
-                        if (RC::valid(c, lane, K)) {
-                          float v[8];
-                          h_.get(c, v);
-                          quant_store8<MODE, true>(qr + RC::col(c, lane), v, s);  // amax from outside: keep the clamp
-                        }
-                      }
-                      if (lane == 0) scale[row] = s.s;
-                    });
+  for (int i = 0; i < NCT; ++i) {
+    const int64_t c = min((int64_t)t + 256 * i, nch - 1);
+    v[i].load(hr + c * 8 * RC::kES, 8, 0);
+  }
+  const RowScale s = scale_from_amax<MODE>(amax_in[row]);
+  char* qr = (char*)q + row * ldq;
+#pragma unroll
+  for (int i = 0; i < NCT; ++i) {
+    const int64_t c = (int64_t)t + 256 * i;
+    if (c < nch) {
+      float f[8];
+      v[i].get(0, f);
+      quant_store8<MODE, true>(qr + c * 8, f, s);  // amax from outside: keep the clamp
+    }
+  }
+  if (t == 0) scale[row] = s.s;
 }
 
 // ---------------------------------------------------------------------------
@@ -290,8 +302,13 @@ template <int MODE, int DT>
 hipError_t launch_quant_rows_amax_t(const void* h, int64_t ldh, const float* amax, int64_t M, int64_t K, void* q,
                                     int64_t ldq, float* scale, hipStream_t st) {
   if (M == 0) return hipSuccess;
-#define L(N, F) hipLaunchKernelGGL((quant_rows_amax_vec<MODE, DT, N, F>), row_grid(quant_rows_amax_vec<MODE, DT, N, F>, M, 0), dim3(256), 0, st, h, ldh, amax, M, K, q, ldq, scale)
-  D3_NCH_DISPATCH(K, L);
+  const int64_t nct = (K / 8 + 255) / 256;  // chunks per thread, K <= kMaxVecK: at most 8
+#define L(N) hipLaunchKernelGGL((quant_rows_amax_stream<MODE, DT, N>), dim3((unsigned)M), dim3(256), 0, st, h, ldh, amax, K, q, ldq, scale)
+  if (nct <= 1) L(1);
+  else if (nct <= 2) L(2);
+  else if (nct <= 4) L(4);
+  else if (nct <= 6) L(6);
+  else L(8);
 #undef L
   return hipGetLastError();
 }
