@@ -49,9 +49,10 @@ namespace d3 {
 
 constexpr int kBK = 128;  // bytes of K per pipeline step
 // M tiles per group of the tile order (XCD-contiguous ranges, then groups of kGroupM M tiles
-// walked N-major): 2 measured 1-2% faster than 4 on all four state-pass shapes (FP8, M = 4096:
-// gate_up 355 -> 352 us, o_proj 63.8 -> 62.4 us), 8 and 16 slower (16: gate_up 382 us).
-constexpr int kGroupM = 2;
+// walked N-major). Measured (FP8, M = 4096): 2 runs 1-1.5% faster than 4 (gate_up 352 vs 355 us) but
+// re-reads each weight panel twice as often (L2-to-fabric traffic of gate_up 1.23 GB vs 0.93 GB);
+// 8 and 16 are slower (16: gate_up 382 us).
+constexpr int kGroupM = 4;
 
 template <int MODE>
 struct Mfma;
