@@ -227,23 +227,36 @@ __global__ __launch_bounds__((CW + 1) * 64, 1) void gemm_w8a8_ws(GemmParams p) {
 }
 
 // Host side: MB row blocks per workgroup (p.tiles_m row parts), p.tiles_n column slabs of 32 NB columns.
-// One consumer per row block; activations 3 blocks deep; the weight ring 8 blocks deep (5 for NB = 4,
-// whose 16 DMAs per block would otherwise pass vmcnt's 63 and LDS).
+// One consumer per row block; activations 3 blocks deep (4 with at most two consumers: o_proj in two
+// row parts 11.0 -> 10.6 us); the weight ring 8 blocks deep (5 for NB = 4, whose 16 DMAs per block
+// would otherwise pass vmcnt's 63 and LDS).
 template <int MODE, int EPI, int OUT, int MB, int NB>
 static hipError_t launch_ws_mb(GemmParams p, hipStream_t st) {
-  constexpr int CW = MB, DW = NB == 4 ? 5 : 8, DA = 3;
+  constexpr int CW = MB, DW = NB == 4 ? 5 : 8, DA = MB <= 2 ? 4 : 3;
   const int64_t slabs8 = ((int64_t)p.tiles_n + 7) / 8 * 8;
   hipLaunchKernelGGL((gemm_w8a8_ws<MODE, MB, NB, CW, DW, DA, EPI, OUT>), dim3((unsigned)(slabs8 * p.tiles_m)),
                      dim3((CW + 1) * 64), 0, st, p);
   return hipGetLastError();
 }
 
+// Row blocks per workgroup: every workgroup reads all K of its rows' activations, and that stream
+// bounds it, so the rows are split into more parts while the slabs x parts still fit one round of
+// CUs (M = 128: o_proj's 128 slabs in two parts of 64 rows, 13.0 -> 10.6 us; QKV's 192 slabs stay
+// whole: two parts would need a second round, 13.7 -> 15.9 us). A row's result does not depend on
+// the split.
+inline int ws_row_blocks(int64_t M, int64_t slabs, int64_t cus) {
+  const int64_t mblocks = (M + 31) / 32;
+  int mb = (int)std::min<int64_t>(mblocks, 4);
+  while (mb > 1 && slabs * ((mblocks + mb / 2 - 1) / (mb / 2)) <= cus) mb /= 2;
+  return mb;
+}
+
 template <int MODE, int EPI, int OUT, int NB>
 static hipError_t launch_ws_nb(GemmParams p, hipStream_t st) {
   const int64_t mblocks = (p.M + 31) / 32;
-  const int mb = (int)std::min<int64_t>(mblocks, 4);
-  p.tiles_m = (int)((mblocks + mb - 1) / mb);
   p.tiles_n = (int)((p.N + 32 * NB - 1) / (32 * NB));
+  const int mb = ws_row_blocks(p.M, p.tiles_n, device_cu_count());
+  p.tiles_m = (int)((mblocks + mb - 1) / mb);
   switch (mb) {
     case 1: return launch_ws_mb<MODE, EPI, OUT, 1, NB>(p, st);
     case 2: return launch_ws_mb<MODE, EPI, OUT, 2, NB>(p, st);
