@@ -106,6 +106,33 @@ def test_graph_replays_match_eager(dev, mode):
         assert torch.equal(out, eager)
 
 
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
+def test_fp16_stack_graph_replays_match_eager(dev, mode):
+    """An fp16 stack: the captured pass takes fp16 rows (its norm weights' dtype), dense and ragged."""
+    st = LinearStack(2, H, QKV, I, mode=mode, dtype=torch.float16, device=dev)
+    st.init_random(torch.Generator(device=dev).manual_seed(21))
+    g = gen(22)
+    x = R.outlier_activations(g, 32, H).to(torch.float16).to(dev)
+    eager = st(x).clone()
+    assert eager.dtype == torch.float16
+    graphed = st.graphed(32)
+    for _ in range(3):
+        st(x)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(graphed(x).clone(), eager)
+    lengths = [16, 5, 0, 11]
+    xr = torch.zeros(len(lengths), 16, H, dtype=torch.float16)
+    for b_, n in enumerate(lengths):
+        if n:
+            xr[b_, :n] = R.outlier_activations(g, n, H).to(torch.float16)
+    xr = xr.to(dev)
+    ragged = st.forward_ragged(xr, lengths).clone()
+    assert torch.equal(st.forward_ragged(xr, lengths, graph=True), ragged)
+    for b_, n in enumerate(lengths):
+        if n:
+            assert torch.equal(ragged[b_, :n], st(xr[b_, :n]))
+
+
 def test_graphed_ragged_pass_equals_eager(dev):
     st = _stack(dev, 2, "int8", 5)
     g = gen(11)
