@@ -14,6 +14,7 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <utility>
@@ -295,19 +296,27 @@ __global__ __launch_bounds__(256) void quant_rows_ragged_vec(
 // host launchers
 // ---------------------------------------------------------------------------
 
+constexpr int64_t kMaxRowBlocks = (int64_t)1 << 30;  // rows per launch of the block-per-row kernels
+
 template <int MODE, int DT>
 hipError_t launch_quant_rows_t(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int64_t ldq,
                                float* scale, bool vec, hipStream_t st) {
   if (M == 0) return hipSuccess;
   if (vec && K <= kMaxVecK) {
     const int64_t nct = (K / 8 + 255) / 256;
-#define L(N) hipLaunchKernelGGL((quant_rows_stream<MODE, DT, N>), dim3((unsigned)M), dim3(256), 0, st, x, ldx, K, q, ldq, scale)
-    if (nct <= 1) L(1);
-    else if (nct <= 2) L(2);
-    else if (nct <= 4) L(4);
-    else if (nct <= 6) L(6);
-    else L(8);
+    // one block per row, in launches of at most kMaxRowBlocks rows (the grid's x limit)
+    for (int64_t r0 = 0; r0 < M; r0 += kMaxRowBlocks) {
+      const unsigned rows = (unsigned)std::min<int64_t>(M - r0, kMaxRowBlocks);
+      const char* xr = (const char*)x + r0 * ldx * (DT == kF32 ? 4 : 2);
+      char* qr = (char*)q + r0 * ldq;
+#define L(N) hipLaunchKernelGGL((quant_rows_stream<MODE, DT, N>), dim3(rows), dim3(256), 0, st, xr, ldx, K, qr, ldq, scale + r0)
+      if (nct <= 1) L(1);
+      else if (nct <= 2) L(2);
+      else if (nct <= 4) L(4);
+      else if (nct <= 6) L(6);
+      else L(8);
 #undef L
+    }
   } else {
     hipLaunchKernelGGL((quant_rows_generic<MODE, DT>), quant_grid(M), dim3(256), 0, st, x, ldx, M, K, q, ldq, scale);
   }
@@ -328,13 +337,18 @@ hipError_t launch_quant_rows_amax_t(const void* h, int64_t ldh, const float* ama
                                     int64_t ldq, float* scale, hipStream_t st) {
   if (M == 0) return hipSuccess;
   const int64_t nct = (K / 8 + 255) / 256;  // chunks per thread, K <= kMaxVecK: at most 8
-#define L(N) hipLaunchKernelGGL((quant_rows_amax_stream<MODE, DT, N>), dim3((unsigned)M), dim3(256), 0, st, h, ldh, amax, K, q, ldq, scale)
-  if (nct <= 1) L(1);
-  else if (nct <= 2) L(2);
-  else if (nct <= 4) L(4);
-  else if (nct <= 6) L(6);
-  else L(8);
+  for (int64_t r0 = 0; r0 < M; r0 += kMaxRowBlocks) {
+    const unsigned rows = (unsigned)std::min<int64_t>(M - r0, kMaxRowBlocks);
+    const char* hr = (const char*)h + r0 * ldh * (DT == kF32 ? 4 : 2);
+    char* qr = (char*)q + r0 * ldq;
+#define L(N) hipLaunchKernelGGL((quant_rows_amax_stream<MODE, DT, N>), dim3(rows), dim3(256), 0, st, hr, ldh, amax + r0, K, qr, ldq, scale + r0)
+    if (nct <= 1) L(1);
+    else if (nct <= 2) L(2);
+    else if (nct <= 4) L(4);
+    else if (nct <= 6) L(6);
+    else L(8);
 #undef L
+  }
   return hipGetLastError();
 }
 
