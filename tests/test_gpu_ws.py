@@ -128,10 +128,10 @@ def test_ws_equals_the_unsplit_128_tile(dev, mode, M, N, Kd):
 
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
 @pytest.mark.parametrize("M", [16, 33, 128])
-@pytest.mark.parametrize("H,I", [(2048, 1536), (512, 12288)])
+@pytest.mark.parametrize("H,I", [(2048, 1536), (512, 12288), (256, 8224)])
 def test_ws_swiglu_equals_the_unsplit_128_tile(dev, mode, M, H, I):
     """Slabs of one gate/up pair (I = 1536) and of two pairs (I = 12288: 64-column slabs would not fit
-    one round of CUs)."""
+    one round of CUs; I = 8224: 257 pairs, so the last two-pair slab holds a single pair)."""
     g = gen(M + 5 * (mode == "fp8") + I)
     mk = rand_i8 if mode == "int8" else rand_fp8
     a, w = mk(g, M, H).to(dev), mk(g, 2 * I, H).to(dev)
