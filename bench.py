@@ -202,7 +202,7 @@ def run_state_pass(args, mode: str):
     def step(_timer=None):
         outs = []
         for name, M, N, K, x, lin in layers:
-            q, s = KK.quantize_rows(x, mode)
+            q, s = KK.quantize_rows(x, mode, kblock=lin.kblock)
             outs.append(KK.gemm(mode, q, s.view(-1), lin.weight, lin.weight_scale,
                                 epilogue=_lib.EPI_DEQUANT, out_dtype=torch.bfloat16))
         return outs
@@ -233,11 +233,12 @@ def run_state_pass(args, mode: str):
     for name, M, N, K, x, lin in layers:
         n_x = max(2, -(-ROTATE_BYTES // x.numel() // x.element_size()))
         xs = [x.clone() for _ in range(n_x)]
-        q, s = KK.quantize_rows(x, mode)
+        q, s = KK.quantize_rows(x, mode, kblock=lin.kblock)
         qb = torch.empty_like(q)
         sb = torch.empty(M, dtype=torch.float32, device=dev)
+        mc, ldq = (KK.mode_code(mode) | _lib.KBLOCK, M) if lin.kblock else (KK.mode_code(mode), K)
         q_us = launch_us(lambda i: _lib.check(_lib.load().d3w8a8_quantize_rows(
-            KK.mode_code(mode), KK.dtype_code(x.dtype), xs[i % n_x].data_ptr(), K, M, K, qb.data_ptr(), K,
+            mc, KK.dtype_code(x.dtype), xs[i % n_x].data_ptr(), K, M, K, qb.data_ptr(), ldq,
             sb.data_ptr(), torch.cuda.current_stream().cuda_stream), "quantize_rows"), 4 * n_x)
         del xs
         n_w = max(2, -(-ROTATE_BYTES // lin.weight.numel()))
@@ -410,9 +411,9 @@ def run_mlp_block(args):
     gu, dn = mlp.gate_up_proj, mlp.down_proj
 
     def step(_t=None):
-        q1, s1, _ = KK.rmsnorm_quantize(x, nw, 1e-6, "int8", clear_amax=amax)
+        q1, s1, _ = KK.rmsnorm_quantize(x, nw, 1e-6, "int8", clear_amax=amax, kblock=True)
         KK.gemm("int8", q1, s1.view(-1), gu.weight, gu.weight_scale, epilogue=_lib.EPI_SWIGLU, out=h, row_amax=amax)
-        q2, s2 = KK.quantize_rows_amax(h, amax, "int8")
+        q2, s2 = KK.quantize_rows_amax(h, amax, "int8", kblock=True)
         return KK.gemm("int8", q2, s2.view(-1), dn.weight, dn.weight_scale, epilogue=_lib.EPI_RESIDUAL,
                        residual=x)
 
@@ -436,7 +437,8 @@ def run_mlp_block(args):
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
     lib = _lib.load()
     k = {}
-    q1, s1, _ = KK.rmsnorm_quantize(x, nw, 1e-6, "int8", clear_amax=amax)
+    q1, s1, _ = KK.rmsnorm_quantize(x, nw, 1e-6, "int8", clear_amax=amax, kblock=True)
+    i8k = KK.mode_code("int8") | _lib.KBLOCK  # K-blocked q, as the block runs it
     for rows in (M, 2 * M):
         xr = x if rows == M else torch.cat([x, x])
         n_x = max(2, -(-ROTATE_BYTES // (rows * H * 2)))
@@ -444,8 +446,8 @@ def run_mlp_block(args):
         qb = torch.empty(rows, H, dtype=torch.int8, device=dev)
         sb = torch.empty(rows, dtype=torch.float32, device=dev)
         us = launch_us(lambda i: _lib.check(lib.d3w8a8_rmsnorm_quantize(
-            KK.mode_code("int8"), KK.dtype_code(x.dtype), xs[i % n_x].data_ptr(), H, KK.dtype_code(nw.dtype),
-            nw.data_ptr(), rows, H, 1e-6, 1, qb.data_ptr(), H, sb.data_ptr(), None, 0, None, st()),
+            i8k, KK.dtype_code(x.dtype), xs[i % n_x].data_ptr(), H, KK.dtype_code(nw.dtype),
+            nw.data_ptr(), rows, H, 1e-6, 1, qb.data_ptr(), rows, sb.data_ptr(), None, 0, None, st()),
             "rmsnorm_quantize"), 4 * n_x)
         nq = quant_bytes(rows, H) + 2 * H
         key = "norm_quant" if rows == M else f"norm_quant_m{rows}"
@@ -462,10 +464,10 @@ def run_mlp_block(args):
                            "frac_peak": round(ops / (us * 1e-6) / 1e12 / PEAK_TOPS["int8"], 4)}
     n_h = max(2, -(-ROTATE_BYTES // (h.numel() * 2)))
     hs = [h.clone() for _ in range(n_h)]
-    q2, s2 = KK.quantize_rows_amax(h, amax, "int8")
+    q2, s2 = KK.quantize_rows_amax(h, amax, "int8", kblock=True)
     us = launch_us(lambda i: _lib.check(lib.d3w8a8_quantize_rows_amax(
-        KK.mode_code("int8"), KK.dtype_code(h.dtype), hs[i % n_h].data_ptr(), I, amax.data_ptr(), M, I,
-        q2.data_ptr(), I, s2.data_ptr(), st()), "quantize_rows_amax"), 4 * n_h)
+        i8k, KK.dtype_code(h.dtype), hs[i % n_h].data_ptr(), I, amax.data_ptr(), M, I,
+        q2.data_ptr(), M, s2.data_ptr(), st()), "quantize_rows_amax"), 4 * n_h)
     del hs
     rq = 2 * M * I + M * I + 4 * M
     k["requant"] = {"us": round(us, 2), "gbs": round(rq / (us * 1e-6) / 1e9, 1),
@@ -530,9 +532,9 @@ def run_gated_quant(args):
     s = torch.empty(M, dtype=torch.float32, device=dev)
     lib = _lib.load()
     us = launch_us(lambda i: _lib.check(lib.d3w8a8_gate_quantize(
-        KK.mode_code("fp8"), KK.dtype_code(torch.bfloat16), outs[i % n].data_ptr(), K, qps[i % n].data_ptr(),
-        2 * K, hd, M, K, q.data_ptr(), K, s.data_ptr(), None, 0, torch.cuda.current_stream().cuda_stream),
-        "gate_quantize"), 4 * n)
+        KK.mode_code("fp8") | _lib.KBLOCK, KK.dtype_code(torch.bfloat16), outs[i % n].data_ptr(), K,
+        qps[i % n].data_ptr(), 2 * K, hd, M, K, q.data_ptr(), M, s.data_ptr(), None, 0,
+        torch.cuda.current_stream().cuda_stream), "gate_quantize"), 4 * n)
     byts = M * K * 2 + M * K * 2 + M * K + 4 * M
     return {"shape": f"{M}x{K}", "head_dim": hd, "us": round(us, 2), "gbs": round(byts / (us * 1e-6) / 1e9, 1),
             "frac_hbm": round(byts / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
@@ -559,8 +561,9 @@ def run_gdn_norm_quant(args):
     s = torch.empty(M, dtype=torch.float32, device=dev)
     lib = _lib.load()
     us = launch_us(lambda i: _lib.check(lib.d3w8a8_gdn_norm_quantize(
-        KK.mode_code("fp8"), KK.dtype_code(torch.bfloat16), xs[i % n].data_ptr(), K, zs[i % n].data_ptr(), K,
-        KK.dtype_code(w.dtype), w.data_ptr(), hd, 1e-6, M, K, q.data_ptr(), K, s.data_ptr(), None, 0,
+        KK.mode_code("fp8") | _lib.KBLOCK, KK.dtype_code(torch.bfloat16), xs[i % n].data_ptr(), K,
+        zs[i % n].data_ptr(), K, KK.dtype_code(w.dtype), w.data_ptr(), hd, 1e-6, M, K, q.data_ptr(), M,
+        s.data_ptr(), None, 0,
         torch.cuda.current_stream().cuda_stream), "gdn_norm_quantize"), 4 * n)
     byts = 2 * M * K * 2 + M * K + 4 * M + 2 * hd
     return {"shape": f"{M}x{K}", "heads": K // hd, "head_dim": hd, "us": round(us, 2),
@@ -654,7 +657,8 @@ def stack_per_shape(stack, gen) -> dict:
     out = {}
     for M in (8192, 128):
         x = torch.randn(M, H, generator=gen, device=dev).to(torch.bfloat16)
-        q_in = (torch.randn(M, I, generator=gen, device=dev) * 8).to(torch.float8_e4m3fn)
+        # K-blocked [K / 64, M, 64], as the stack's quantize kernels write them
+        q_in = (torch.randn(I // 64, M, 64, generator=gen, device=dev) * 8).to(torch.float8_e4m3fn)
         s_in = torch.rand(M, generator=gen, device=dev) * 1e-3
         qkv = torch.empty(M, Q, dtype=torch.bfloat16, device=dev)
         hbuf = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
@@ -662,7 +666,7 @@ def stack_per_shape(stack, gen) -> dict:
         o = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
         qb = torch.empty(M, I, dtype=torch.float8_e4m3fn, device=dev)
         sb = torch.empty(M, dtype=torch.float32, device=dev)
-        a4 = q_in[:, :H]
+        a4 = q_in[: H // 64]
         gemms = {
             "qkv": (lambda i: KK.gemm("fp8", a4, s_in, L[i % n].qkv_proj.weight, L[i % n].qkv_proj.weight_scale,
                                       out=qkv), Q, H, 0),
@@ -691,15 +695,16 @@ def stack_per_shape(stack, gen) -> dict:
         xs = [torch.randn(M, H, generator=gen, device=dev).to(torch.bfloat16) for _ in range(4)]
         hs = [torch.randn(M, I, generator=gen, device=dev).to(torch.bfloat16) for _ in range(2)]
         amax_h = torch.full((M,), 4.0, device=dev)
+        f8k = KK.mode_code("fp8") | _lib.KBLOCK  # K-blocked q, as the stack writes it
         quant = {
             "norm+quantize": (lambda i: _lib.check(lib.d3w8a8_rmsnorm_quantize(
-                1, 0, xs[i % 4].data_ptr(), H, 0, L[i % n].input_layernorm.data_ptr(), M, H, 1e-6, 1,
-                qb.data_ptr(), H, sb.data_ptr(), None, 0, None, st()), "norm"), quant_bytes(M, H) + 2 * H),
+                f8k, 0, xs[i % 4].data_ptr(), H, 0, L[i % n].input_layernorm.data_ptr(), M, H, 1e-6, 1,
+                qb.data_ptr(), M, sb.data_ptr(), None, 0, None, st()), "norm"), quant_bytes(M, H) + 2 * H),
             "quantize(q block)": (lambda i: _lib.check(lib.d3w8a8_quantize_rows(
-                1, 0, xs[i % 4].data_ptr(), H, M, H, qb.data_ptr(), H, sb.data_ptr(), st()), "quant"),
+                f8k, 0, xs[i % 4].data_ptr(), H, M, H, qb.data_ptr(), M, sb.data_ptr(), st()), "quant"),
                 quant_bytes(M, H)),
             "requantize(h)": (lambda i: _lib.check(lib.d3w8a8_quantize_rows_amax(
-                1, 0, hs[i % 2].data_ptr(), I, amax_h.data_ptr(), M, I, qb.data_ptr(), I, sb.data_ptr(), st()),
+                f8k, 0, hs[i % 2].data_ptr(), I, amax_h.data_ptr(), M, I, qb.data_ptr(), M, sb.data_ptr(), st()),
                 "requant"), quant_bytes(M, I)),
         }
         for name, (fn, byts) in quant.items():
@@ -734,7 +739,8 @@ def run_question_gemms(args):
         copies = max(2, -(-(600 << 20) // (N * Kd)))
         ws = [(torch.randn(N, Kd, generator=gen, device=dev) * 8).to(torch.float8_e4m3fn) for _ in range(copies)]
         w_s = torch.rand(N, generator=gen, device=dev) * 1e-3
-        a = (torch.randn(M, Kd, generator=gen, device=dev) * 8).to(torch.float8_e4m3fn)
+        # K-blocked activations [K / 64, M, 64], as the module's quantize kernels hand them to the GEMM
+        a = (torch.randn(Kd // 64, M, 64, generator=gen, device=dev) * 8).to(torch.float8_e4m3fn)
         a_s = torch.rand(M, generator=gen, device=dev) * 1e-3
         y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
         res = {"M": M, "N": N, "K": Kd}
@@ -840,7 +846,7 @@ def single_pass(mode: str) -> int:
     torch.cuda.synchronize()
     del src, flush, dst
     for _, M, N, K, x, lin in layers:
-        q, s = KK.quantize_rows(x, mode)
+        q, s = KK.quantize_rows(x, mode, kblock=lin.kblock)
         KK.gemm(mode, q, s.view(-1), lin.weight, lin.weight_scale, epilogue=_lib.EPI_DEQUANT,
                 out_dtype=torch.bfloat16)
     torch.cuda.synchronize()

@@ -368,6 +368,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, ACC (&acc)[TM][TN]
   epilogue<MODE, TM, TN, EPI, OUT, false>(p, acc, wrow0, wcol0, lane, stage, [] {});
 }
 
+// Register-staged tiles: row-major A only (plan_gemm never gives them a K-blocked A).
 template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
 __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8(GemmParams p) {
   using MF = Mfma<MODE>;
@@ -720,22 +721,25 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   const int lrow = lane & 31, lhalf = lane >> 5;
 
   // DMA sources: uniform tile bases + per-lane 32-bit offsets (the host keeps every operand
-  // offset below 2^32 for this kernel)
+  // offset below 2^32 for this kernel). A is row-major or K-blocked (QDst, kernels.hpp): byte (m, k)
+  // at m * a_rs + (k / 64) * a_bs + k % 64.
   const uint8_t* a_base;
   const uint8_t* b_base;
   uint32_t a_off[A_DMA], b_off[B_DMA];
+  const int64_t a_rs = p.a_kblk ? 64 : p.lda, a_bs = p.a_kblk ? 64 * p.lda : 64;
+  const int64_t a_step = (BK / 64) * a_bs;  // A bytes per K step
   auto setup = [&](int t) {
     if constexpr (kSplitTile<BM, BN>) tile_of(t, (int)gridDim.x / S, p.tiles_m, p.tiles_n, tm, tn);
     else tile_of(t, ntiles, p.tiles_m, p.tiles_n, tm, tn);
     m0 = (int64_t)tm * BM;
     n0 = (int64_t)tn * BN;
-    a_base = uniform_ptr(p.a + m0 * p.lda + (int64_t)kbeg * BK);
+    a_base = uniform_ptr(p.a + m0 * a_rs + (int64_t)kbeg * a_step);
     b_base = uniform_ptr(p.w + n0 * p.ldw + (int64_t)kbeg * BK);
 #pragma unroll
     for (int i = 0; i < A_DMA; ++i) {
       const int row = (i * NW + wave) * RPD + lane / CPR;
-      const int ch = (lane % CPR) ^ lds_swz<BK>(row);
-      a_off[i] = (uint32_t)((min(m0 + row, p.M - 1) - m0) * p.lda + ch * 16);
+      const int ch = (lane % CPR) ^ lds_swz<BK>(row);  // logical 16-byte chunk of the step's K bytes
+      a_off[i] = (uint32_t)((min(m0 + row, p.M - 1) - m0) * a_rs + (ch >> 2) * a_bs + (ch & 3) * 16);
     }
 #pragma unroll
     for (int i = 0; i < B_DMA; ++i) {
@@ -751,9 +755,8 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   // DMA d of step kt into stage U
   auto dma_one = [&](auto u_c, auto d_c, int kt) {
     constexpr int U = decltype(u_c)::value % kStages, d = decltype(d_c)::value;
-    const int64_t kb = (int64_t)kt * BK;
-    if constexpr (d < A_DMA) dma16<U * STAGE + d * NW * 1024>(a_base + kb, a_off[d], lds_wave);
-    else dma16<U * STAGE + A_BYTES + (d - A_DMA) * NW * 1024>(b_base + kb, b_off[d - A_DMA], lds_wave);
+    if constexpr (d < A_DMA) dma16<U * STAGE + d * NW * 1024>(a_base + (int64_t)kt * a_step, a_off[d], lds_wave);
+    else dma16<U * STAGE + A_BYTES + (d - A_DMA) * NW * 1024>(b_base + (int64_t)kt * BK, b_off[d - A_DMA], lds_wave);
   };
   auto dma_stage = [&](auto u_c, int kt) { static_for<0, DPS>([&](auto d_c) { dma_one(u_c, d_c, kt); }); };
 

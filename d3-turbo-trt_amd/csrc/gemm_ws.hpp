@@ -140,23 +140,29 @@ __global__ __launch_bounds__((CW + 1) * 64, 1) void gemm_w8a8_ws(GemmParams p) {
   // ---------------- consumer c: row blocks c RB .. c RB + RB - 1 ----------------
   const int c = wave;
   const int64_t r0 = m0 + 32 * RB * c;  // first row of this consumer
+  // A row-major or K-blocked (QDst, kernels.hpp): byte (m, k) at m * a_rs + (k / 64) * a_bs + k % 64;
+  // a 128-byte block spans two 64-byte K blocks
+  const int64_t a_rs = p.a_kblk ? 64 : p.lda, a_bs = p.a_kblk ? 64 * p.lda : 64;
   uint32_t a_off[ADMA];
 #pragma unroll
   for (int d = 0; d < ADMA; ++d) {
     const int row = 8 * d + (lane >> 3);
     const int ch = (lane & 7) ^ lds_swz<kWsKB>(row);
-    a_off[d] = (uint32_t)((min(r0 + row, p.M - 1) - r0) * p.lda + ch * 16);
+    a_off[d] = (uint32_t)((min(r0 + row, p.M - 1) - r0) * a_rs + (ch >> 2) * a_bs + (ch & 3) * 16);
   }
   // rows past M read row M - 1; if this consumer's first row is past M it still runs the loop (the
   // barriers are shared) on clamped rows and stores nothing
-  const uint8_t* a_rows = p.a + min(r0, p.M - 1) * p.lda;
+  const uint8_t* a_rows = p.a + min(r0, p.M - 1) * a_rs;
   if (r0 >= p.M) {
 #pragma unroll
-    for (int d = 0; d < ADMA; ++d) a_off[d] = (uint32_t)((lane & 7) ^ lds_swz<kWsKB>(8 * d + (lane >> 3))) * 16;
+    for (int d = 0; d < ADMA; ++d) {
+      const int ch = (lane & 7) ^ lds_swz<kWsKB>(8 * d + (lane >> 3));
+      a_off[d] = (uint32_t)((ch >> 2) * a_bs + (ch & 3) * 16);
+    }
   }
   const uint32_t aring = lds0 + (uint32_t)C::W_BYTES + (uint32_t)c * (uint32_t)(DA * C::ABLK);
   auto issue_a = [&](int t) {
-    const uint8_t* g = uniform_ptr(a_rows + (int64_t)t * kWsKB);
+    const uint8_t* g = uniform_ptr(a_rows + (int64_t)t * 2 * a_bs);
     const uint32_t slot = aring + (uint32_t)(t % DA) * C::ABLK;
     static_for<0, ADMA>([&](auto d_c) {
       constexpr int d = decltype(d_c)::value;

@@ -6,9 +6,33 @@
 
 namespace d3 {
 
+// Layouts of quantized activations. Row-major: byte (m, k) at m * ld + k. K-blocked: each 64-byte
+// slice of K holds all rows back to back, byte (m, k) at ((k / 64) * ld + m) * 64 + k % 64 (ld >= M:
+// the row capacity). A pipelined GEMM tile loads 64 bytes of K from each of its rows per step; row-major
+// rows make each load half a 128-byte line of many rows, K-blocked rows make it whole lines of
+// consecutive rows (MI355X, FP8 256x256 tile at M = 4096: gate_up 354 -> 329 us, down 155 -> 137 us).
+// Both are addressed as row * rs + (k / 64) * bs + k % 64.
+struct QDst {
+  char* q;
+  int64_t rs;  // bytes between rows
+  int64_t bs;  // bytes between 64-byte K blocks
+  static QDst of(void* q, int64_t ld, bool kblk) {
+    return kblk ? QDst{(char*)q, 64, 64 * ld} : QDst{(char*)q, ld, 64};
+  }
+  __host__ __device__ QDst rows_from(int64_t r0) const { return QDst{q + r0 * rs, rs, bs}; }
+  // K-blocked with room for more than one row (a one-row K-blocked q is also row-major)
+  __host__ __device__ bool kblocked() const { return rs == 64 && bs > 64; }
+  __device__ __forceinline__ char* row(int64_t r) const { return q + r * rs; }
+  // column col (a multiple of 8 for the vector stores: an 8-byte store stays in one K block)
+  __device__ __forceinline__ static char* at(char* qrow, int64_t col, int64_t bs) {
+    return qrow + (col >> 6) * bs + (col & 63);
+  }
+};
+
 struct GemmParams {
   const uint8_t* a;
-  int64_t lda;
+  int64_t lda;  // row-major: elements between rows; K-blocked (a_kblk): the row capacity (>= M)
+  int a_kblk;   // A is K-blocked (pipelined tiles only)
   const float* a_scale;
   const uint8_t* w;
   int64_t ldw;
@@ -30,22 +54,22 @@ struct GemmParams {
   uint32_t* partial;  // tiles * ksplit * BM * BN 32-bit words
 };
 
-hipError_t launch_quant_rows(int mode, int dt, const void* x, int64_t ldx, int64_t M, int64_t K, void* q,
-                             int64_t ldq, float* scale, bool vec, hipStream_t st);
+hipError_t launch_quant_rows(int mode, int dt, const void* x, int64_t ldx, int64_t M, int64_t K, QDst q,
+                             float* scale, bool vec, hipStream_t st);
 hipError_t launch_quant_rows_amax(int mode, int dt, const void* h, int64_t ldh, const float* amax, int64_t M,
-                                  int64_t K, void* q, int64_t ldq, float* scale, hipStream_t st);
+                                  int64_t K, QDst q, float* scale, hipStream_t st);
 hipError_t launch_rmsnorm_quant(int mode, int dt, int dtw, const void* x, int64_t ldx, const void* w, int64_t M,
-                                int64_t K, float eps, int zc, void* q, int64_t ldq, float* scale, void* normed,
+                                int64_t K, float eps, int zc, QDst q, float* scale, void* normed,
                                 int64_t ldn, float* clear_amax, hipStream_t st);
 // o_proj input of a gated attention layer: quantize_rows(x * sigmoid(gate)); head_dim > 0 reads the
 // gate in place from the per-head [query | gate] rows of the q_proj output. 16-bit inputs only.
 hipError_t launch_gate_quant(int mode, int dt, const void* x, int64_t ldx, const void* gate, int64_t ldg,
-                             int64_t head_dim, int64_t M, int64_t K, void* q, int64_t ldq, float* scale, void* y_out,
+                             int64_t head_dim, int64_t M, int64_t K, QDst q, float* scale, void* y_out,
                              int64_t ldy, hipStream_t st);
 // GDN output: gated RMSNorm over heads of head_dim (64, 128, 256 or 512), then quantize_rows over the
 // whole row. 16-bit inputs; w is head_dim entries of the input dtype or fp32.
 hipError_t launch_gdn_norm_quant(int mode, int dt, int dtw, const void* x, int64_t ldx, const void* z, int64_t ldz,
-                                 const void* w, int head_dim, float eps, int64_t M, int64_t K, void* q, int64_t ldq,
+                                 const void* w, int head_dim, float eps, int64_t M, int64_t K, QDst q,
                                  float* scale, void* y_out, int64_t ldy, hipStream_t st);
 // Packed-row offsets of a ragged batch, passed by value in the kernel arguments:
 // segment b owns packed rows [off[b], off[b + 1]).
@@ -55,7 +79,7 @@ struct SegOffsets {
 };
 
 hipError_t launch_quant_ragged(int mode, int dt, int out_es, const void* x, int64_t ldx, const SegOffsets& segs,
-                               int64_t nseg, int64_t width, int64_t K, void* q, int64_t ldq, float* scale,
+                               int64_t nseg, int64_t width, int64_t K, QDst q, float* scale,
                                int32_t* row_map, void* out, int64_t ldo, int64_t N, hipStream_t st);
 enum TileCfg : int {
   kTileAuto = -1,
@@ -82,9 +106,14 @@ struct GemmPlan {
   int64_t ws_bytes;  // workspace the plan uses (0 when ksplit == 1)
   const char* error; // non-null: the request is not valid
 };
-// `epi` (an Epilogue) rules out tiles the epilogue cannot use.
+// `epi` (an Epilogue) rules out tiles the epilogue cannot use; a K-blocked A (`a_kblk`) rules out the
+// register-staged tiles.
 GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
-                   int64_t ws_bytes, int epi);
+                   int64_t ws_bytes, int epi, bool a_kblk = false);
+
+// Largest row capacity of a K-blocked A: the pipelined tiles keep per-lane offsets (two K blocks apart
+// at most) below 2^32.
+constexpr int64_t kMaxKblkRows = (int64_t)1 << 25;
 // Launches the plan; p.partial must point to a workspace of plan.ws_bytes.
 hipError_t launch_gemm(int mode, GemmParams p, int epi, int out_dt, const GemmPlan& plan, hipStream_t st);
 

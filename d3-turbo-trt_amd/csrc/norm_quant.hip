@@ -18,7 +18,7 @@ namespace d3 {
 template <int MODE, int DT, int DTW, int NCH, bool FULL>
 __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
     const void* __restrict__ x, int64_t ldx, const void* __restrict__ w, int64_t M, int64_t K,
-    float eps, int zc, void* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+    float eps, int zc, const QDst qd, float* __restrict__ scale,
     void* __restrict__ normed, int64_t ldn, float* __restrict__ clear_amax) {
   extern __shared__ __attribute__((aligned(16))) float gain_lds[];  // K floats: g = 1 + w (zc) or w
   const int lane = threadIdx.x & 63;
@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
         }
         const RowScale s = scale_from_amax<MODE>(wave_max(amax));
         if constexpr (NCH > 12) y.fence();  // wide rows: keep y packed between the passes (registers)
-        char* qr = (char*)q + row * ldq;
+        char* qr = qd.row(row);
         char* nr = normed ? (char*)normed + row * ldn * RC::kES : nullptr;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
             const int64_t col = RC::col(c, lane);
             float v[8];
             y.get(c, v);
-            quant_store8<MODE>(qr + col, v, s);
+            quant_store8<MODE>(QDst::at(qr, col, qd.bs), v, s);
             if (nr) y.store_raw(c, nr + col * RC::kES);
           }
         }
@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
 template <int MODE, int DT, int DTW, int NCT>
 __global__ __launch_bounds__(256) void rmsnorm_quant_rowblock(
     const void* __restrict__ x, int64_t ldx, const void* __restrict__ w, int64_t K, float eps, int zc,
-    void* __restrict__ q, int64_t ldq, float* __restrict__ scale, void* __restrict__ normed, int64_t ldn,
+    const QDst qd, float* __restrict__ scale, void* __restrict__ normed, int64_t ldn,
     float* __restrict__ clear_amax) {
   using RC = RowChunks<DT, 1, true>;
   using RW = RowChunks<DTW, 1, true>;
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_rowblock(
   __syncthreads();
   amax = amax_join(amax_join(red[1][0], red[1][1]), amax_join(red[1][2], red[1][3]));
   const RowScale s = scale_from_amax<MODE>(amax);
-  char* qr = (char*)q + row * ldq;
+  char* qr = qd.row(row);
   char* nr = normed ? (char*)normed + row * ldn * RC::kES : nullptr;
 #pragma unroll
   for (int i = 0; i < NCT; ++i) {
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_rowblock(
     if (c < nch) {
       float v[8];
       y[i].get(0, v);
-      quant_store8<MODE>(qr + c * 8, v, s);
+      quant_store8<MODE>(QDst::at(qr, c * 8, qd.bs), v, s);
       if (nr) y[i].store_raw(0, nr + c * 8 * RC::kES);
     }
   }
@@ -267,7 +267,7 @@ __device__ __forceinline__ float group_sum(float v, int group) {
 template <int MODE, int DT, int DTW, int NCH, bool FULL>
 __global__ __launch_bounds__(256) void gdn_norm_quant_vec(
     const void* __restrict__ x, int64_t ldx, const void* __restrict__ z, int64_t ldz, const void* __restrict__ w,
-    int head_dim, float eps, int64_t M, int64_t K, void* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+    int head_dim, float eps, int64_t M, int64_t K, const QDst qd, float* __restrict__ scale,
     void* __restrict__ y_out, int64_t ldy) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
@@ -329,14 +329,14 @@ __global__ __launch_bounds__(256) void gdn_norm_quant_vec(
   }
   const RowScale s = scale_from_amax<MODE>(wave_max(amax));
   if constexpr (NCH > 12) y.fence();
-  char* qr = (char*)q + row * ldq;
+  char* qr = qd.row(row);
   char* yr = y_out ? (char*)y_out + row * ldy * RC::kES : nullptr;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     if (RC::valid(c, lane, K)) {
       float v[8];
       y.get(c, v);
-      quant_store8<MODE>(qr + RC::col(c, lane), v, s);
+      quant_store8<MODE>(QDst::at(qr, RC::col(c, lane), qd.bs), v, s);
       if (yr) y.store_raw(c, yr + RC::col(c, lane) * RC::kES);
     }
   }
@@ -345,20 +345,20 @@ __global__ __launch_bounds__(256) void gdn_norm_quant_vec(
 
 template <int MODE, int DT, int DTW>
 hipError_t launch_gdn_norm_quant_t(const void* x, int64_t ldx, const void* z, int64_t ldz, const void* w,
-                                   int head_dim, float eps, int64_t M, int64_t K, void* q, int64_t ldq, float* scale,
+                                   int head_dim, float eps, int64_t M, int64_t K, QDst q, float* scale,
                                    void* y_out, int64_t ldy, hipStream_t st) {
   if (M == 0) return hipSuccess;
-#define L(N, F) hipLaunchKernelGGL((gdn_norm_quant_vec<MODE, DT, DTW, N, F>), quant_grid(M), dim3(256), 0, st, x, ldx, z, ldz, w, head_dim, eps, M, K, q, ldq, scale, y_out, ldy)
+#define L(N, F) hipLaunchKernelGGL((gdn_norm_quant_vec<MODE, DT, DTW, N, F>), quant_grid(M), dim3(256), 0, st, x, ldx, z, ldz, w, head_dim, eps, M, K, q, scale, y_out, ldy)
   D3_NCH_DISPATCH(K, L);
 #undef L
   return hipGetLastError();
 }
 
 hipError_t launch_gdn_norm_quant(int mode, int dt, int dtw, const void* x, int64_t ldx, const void* z, int64_t ldz,
-                                 const void* w, int head_dim, float eps, int64_t M, int64_t K, void* q, int64_t ldq,
+                                 const void* w, int head_dim, float eps, int64_t M, int64_t K, QDst q,
                                  float* scale, void* y_out, int64_t ldy, hipStream_t st) {
   if (K > kMaxVecK) return hipErrorInvalidValue;
-#define C(MO, D, W) if (mode == MO && dt == D && dtw == W) return launch_gdn_norm_quant_t<MO, D, W>(x, ldx, z, ldz, w, head_dim, eps, M, K, q, ldq, scale, y_out, ldy, st)
+#define C(MO, D, W) if (mode == MO && dt == D && dtw == W) return launch_gdn_norm_quant_t<MO, D, W>(x, ldx, z, ldz, w, head_dim, eps, M, K, q, scale, y_out, ldy, st)
   C(kInt8, kBF16, kBF16); C(kInt8, kBF16, kF32); C(kInt8, kF16, kF16); C(kInt8, kF16, kF32);
   C(kFp8, kBF16, kBF16); C(kFp8, kBF16, kF32); C(kFp8, kF16, kF16); C(kFp8, kF16, kF32);
 #undef C
@@ -373,14 +373,14 @@ constexpr int64_t kNormRowBlockMaxRows = D3_NORM_ROWBLOCK_MAX;
 
 template <int MODE, int DT, int DTW>
 hipError_t launch_rmsnorm_quant_t(const void* x, int64_t ldx, const void* w, int64_t M, int64_t K, float eps,
-                                  int zc, void* q, int64_t ldq, float* scale, void* normed, int64_t ldn,
+                                  int zc, QDst q, float* scale, void* normed, int64_t ldn,
                                   float* clear_amax, hipStream_t st) {
   if (M == 0) return hipSuccess;
   if (M <= kNormRowBlockMaxRows) {
     const int64_t nct = (K / 8 + 255) / 256;  // chunks per thread, K <= kMaxVecK: at most 8
 #define R(N)                                                                                                 \
   hipLaunchKernelGGL((rmsnorm_quant_rowblock<MODE, DT, DTW, N>), dim3((unsigned)M), dim3(256), 0, st, x, ldx, w, K, \
-                     eps, zc, q, ldq, scale, normed, ldn, clear_amax)
+                     eps, zc, q, scale, normed, ldn, clear_amax)
     if (nct <= 1) R(1);
     else if (nct <= 2) R(2);
     else if (nct <= 4) R(4);
@@ -393,17 +393,17 @@ hipError_t launch_rmsnorm_quant_t(const void* x, int64_t ldx, const void* w, int
 #define L(N, F)                                                                                               \
   hipLaunchKernelGGL((rmsnorm_quant_vec<MODE, DT, DTW, N, F>),                                                 \
                      row_grid(rmsnorm_quant_vec<MODE, DT, DTW, N, F>, M, lds, kNormRowBlocksPerCU),             \
-                     dim3(256), lds, st, x, ldx, w, M, K, eps, zc, q, ldq, scale, normed, ldn, clear_amax)
+                     dim3(256), lds, st, x, ldx, w, M, K, eps, zc, q, scale, normed, ldn, clear_amax)
   D3_NCH_DISPATCH(K, L);
 #undef L
   return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm_quant(int mode, int dt, int dtw, const void* x, int64_t ldx, const void* w, int64_t M,
-                                int64_t K, float eps, int zc, void* q, int64_t ldq, float* scale, void* normed,
+                                int64_t K, float eps, int zc, QDst q, float* scale, void* normed,
                                 int64_t ldn, float* clear_amax, hipStream_t st) {
   if (K > kMaxVecK) return hipErrorInvalidValue;
-#define C(MO, D, W) if (mode == MO && dt == D && dtw == W) return launch_rmsnorm_quant_t<MO, D, W>(x, ldx, w, M, K, eps, zc, q, ldq, scale, normed, ldn, clear_amax, st)
+#define C(MO, D, W) if (mode == MO && dt == D && dtw == W) return launch_rmsnorm_quant_t<MO, D, W>(x, ldx, w, M, K, eps, zc, q, scale, normed, ldn, clear_amax, st)
   C(kInt8, kBF16, kBF16); C(kInt8, kBF16, kF32); C(kInt8, kF16, kF16); C(kInt8, kF16, kF32); C(kInt8, kF32, kF32);
   C(kFp8, kBF16, kBF16); C(kFp8, kBF16, kF32); C(kFp8, kF16, kF16); C(kFp8, kF16, kF32); C(kFp8, kF32, kF32);
 #undef C

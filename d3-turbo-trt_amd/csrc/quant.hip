@@ -56,7 +56,8 @@ int device_cu_count() {
 }
 
 // ---------------------------------------------------------------------------
-// quantize_rows: x [M, K] (ld ldx) -> q [M, K] (ld ldq) + scale [M]
+// quantize_rows: x [M, K] (ld ldx) -> q [M, K] + scale [M]; q is row-major
+// or K-blocked (QDst, kernels.hpp).
 // Vector path: K % 8 == 0, rows 16B aligned.
 // ---------------------------------------------------------------------------
 // One 256-thread block per row: thread t takes the 8-element chunks t, t + 256,
@@ -69,8 +70,7 @@ int device_cu_count() {
 // one row prefetched.
 template <int MODE, int DT, int NCT>
 __global__ __launch_bounds__(256) void quant_rows_stream(const void* __restrict__ x, int64_t ldx, int64_t K,
-                                                        void* __restrict__ q, int64_t ldq,
-                                                        float* __restrict__ scale) {
+                                                        const QDst qd, float* __restrict__ scale) {
   using RC = RowChunks<DT, 1, true>;
   __shared__ float red[kQuantWaves];
   const int64_t row = blockIdx.x;
@@ -92,24 +92,92 @@ __global__ __launch_bounds__(256) void quant_rows_stream(const void* __restrict_
   __syncthreads();
   m = amax_join(amax_join(red[0], red[1]), amax_join(red[2], red[3]));
   const RowScale s = scale_from_amax<MODE>(m);
-  char* qr = (char*)q + row * ldq;
+  char* qr = qd.row(row);
 #pragma unroll
   for (int i = 0; i < NCT; ++i) {
     const int64_t c = (int64_t)t + 256 * i;
     if (c < nch) {
       float f[8];
       v[i].get(0, f);
-      quant_store8<MODE>(qr + c * 8, f, s);
+      quant_store8<MODE>(QDst::at(qr, c * 8, qd.bs), f, s);
     }
   }
   if (t == 0) scale[row] = s.s;
 }
 
+// ---------------------------------------------------------------------------
+// K-blocked q (QDst, kernels.hpp): two rows per block. In that layout the 64-byte K block of rows 2p
+// and 2p + 1 is one 128-byte line; with one row per block every line would be written in two halves
+// by two blocks (FP8, 4096 x 4096 bf16: 10.5 -> 12.2 us; requantize 4096 x 12288: 25.5 -> 33.6 us).
+// Here lane l of wave w takes row 2p + l / 32 and the 8-element chunks (l % 32) + 32 w + 128 i, so
+// each store instruction writes K blocks of both rows: whole lines. The row amax is reduced over the
+// lanes of the row's half wave (DPP) and then over the four waves through LDS; AMAX_IN takes it from
+// the SwiGLU epilogue instead (requantization). A missing second row (odd M) re-reads the last row
+// and stores nothing.
+// ---------------------------------------------------------------------------
+// max over each half wave (lanes 0-31, 32-63) of values >= 0, returned to the lanes of that half
+__device__ __forceinline__ float half_wave_max(float v, int lane) {
+  const auto join = [](float a, float b) { return amax_join(a, b); };
+  v = join(v, dpp_f32<0x111, 0xf>(v));  // row_shr:1
+  v = join(v, dpp_f32<0x112, 0xf>(v));  // row_shr:2
+  v = join(v, dpp_f32<0x114, 0xf>(v));  // row_shr:4
+  v = join(v, dpp_f32<0x118, 0xf>(v));  // row_shr:8
+  v = join(v, dpp_f32<0x142, 0xa>(v));  // row_bcast:15 into rows 1 and 3: lane 31 holds lanes 0-31, lane 63 32-63
+  const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+  const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+  return lane < 32 ? lo : hi;
+}
+
+template <int MODE, int DT, int NCT, bool AMAX_IN>
+__global__ __launch_bounds__(256) void quant_rows_pair(const void* __restrict__ x, int64_t ldx,
+                                                      const float* __restrict__ amax_in, int64_t M, int64_t K,
+                                                      const QDst qd, float* __restrict__ scale) {
+  using RC = RowChunks<DT, 1, true>;
+  __shared__ float red[2][kQuantWaves];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, half = lane >> 5, j = lane & 31;
+  const int64_t row = 2 * (int64_t)blockIdx.x + half;
+  const int64_t rrow = min(row, M - 1);
+  const int64_t nch = K / 8;
+  const char* xr = (const char*)x + rrow * ldx * RC::kES;
+  RC v[NCT];
+#pragma unroll
+  for (int i = 0; i < NCT; ++i) {
+    const int64_t c = min((int64_t)j + 32 * wave + 128 * i, nch - 1);
+    v[i].load(xr + c * 8 * RC::kES, 8, 0);
+  }
+  float m;
+  if constexpr (AMAX_IN) {
+    m = amax_in[rrow];
+  } else {
+    m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NCT; ++i)
+      if (j + 32 * wave + 128 * i < nch) m = amax_join(m, v[i].amax(8, 0));
+    m = half_wave_max(m, lane);
+    if (j == 0) red[half][wave] = m;
+    __syncthreads();
+    m = amax_join(amax_join(red[half][0], red[half][1]), amax_join(red[half][2], red[half][3]));
+  }
+  const RowScale s = scale_from_amax<MODE>(m);
+  if (row >= M) return;
+  char* qr = qd.row(row);
+#pragma unroll
+  for (int i = 0; i < NCT; ++i) {
+    const int64_t c = (int64_t)j + 32 * wave + 128 * i;
+    if (c < nch) {
+      float f[8];
+      v[i].get(0, f);
+      quant_store8<MODE, AMAX_IN>(QDst::at(qr, c * 8, qd.bs), f, s);  // amax from outside: keep the clamp
+    }
+  }
+  if (wave == 0 && j == 0) scale[row] = s.s;
+}
+
 // Generic path for any K / alignment: two passes over the row (amax, then quantize).
 template <int MODE, int DT>
 __global__ __launch_bounds__(256) void quant_rows_generic(const void* __restrict__ x, int64_t ldx,
-                                                         int64_t M, int64_t K, void* __restrict__ q,
-                                                         int64_t ldq, float* __restrict__ scale) {
+                                                         int64_t M, int64_t K, const QDst qd,
+                                                         float* __restrict__ scale) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
   if (row >= M) return;
@@ -118,11 +186,12 @@ __global__ __launch_bounds__(256) void quant_rows_generic(const void* __restrict
   for (int64_t k = lane; k < K; k += 64) amax = amax_acc(amax, load_elem<DT>(x, base + k));
   amax = wave_max(amax);
   const RowScale s = scale_from_amax<MODE>(amax);
-  uint8_t* qr = (uint8_t*)q + row * ldq;
+  char* qr = qd.row(row);
   for (int64_t k = lane; k < K; k += 64) {
     const float xv = load_elem<DT>(x, base + k);
-    if constexpr (MODE == kInt8) qr[k] = (uint8_t)quant_i8_bits<false>(xv, s);
-    else qr[k] = (uint8_t)(quant_f8_pair(xv, 0.0f, s) & 0xff);
+    uint8_t* qk = (uint8_t*)QDst::at(qr, k, qd.bs);
+    if constexpr (MODE == kInt8) *qk = (uint8_t)quant_i8_bits<false>(xv, s);
+    else *qk = (uint8_t)(quant_f8_pair(xv, 0.0f, s) & 0xff);
   }
   if (lane == 0) scale[row] = s.s;
 }
@@ -140,8 +209,7 @@ __global__ __launch_bounds__(256) void quant_rows_generic(const void* __restrict
 template <int MODE, int DT, int NCT>
 __global__ __launch_bounds__(256) void quant_rows_amax_stream(const void* __restrict__ h, int64_t ldh,
                                                              const float* __restrict__ amax_in, int64_t K,
-                                                             void* __restrict__ q, int64_t ldq,
-                                                             float* __restrict__ scale) {
+                                                             const QDst qd, float* __restrict__ scale) {
   using RC = RowChunks<DT, 1, true>;
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x;
@@ -154,14 +222,14 @@ __global__ __launch_bounds__(256) void quant_rows_amax_stream(const void* __rest
     v[i].load(hr + c * 8 * RC::kES, 8, 0);
   }
   const RowScale s = scale_from_amax<MODE>(amax_in[row]);
-  char* qr = (char*)q + row * ldq;
+  char* qr = qd.row(row);
 #pragma unroll
   for (int i = 0; i < NCT; ++i) {
     const int64_t c = (int64_t)t + 256 * i;
     if (c < nch) {
       float f[8];
       v[i].get(0, f);
-      quant_store8<MODE, true>(qr + c * 8, f, s);  // amax from outside: keep the clamp
+      quant_store8<MODE, true>(QDst::at(qr, c * 8, qd.bs), f, s);  // amax from outside: keep the clamp
     }
   }
   if (t == 0) scale[row] = s.s;
@@ -184,7 +252,7 @@ __global__ __launch_bounds__(256) void quant_rows_amax_stream(const void* __rest
 template <int MODE, int DT, int NCH, bool FULL>
 __global__ __launch_bounds__(256) void gate_quant_vec(const void* __restrict__ x, int64_t ldx,
                                                      const void* __restrict__ gate, int64_t ldg, int64_t head_dim,
-                                                     int64_t M, int64_t K, void* __restrict__ q, int64_t ldq,
+                                                     int64_t M, int64_t K, const QDst qd,
                                                      float* __restrict__ scale, void* __restrict__ y_out,
                                                      int64_t ldy) {
   const int lane = threadIdx.x & 63;
@@ -228,14 +296,14 @@ __global__ __launch_bounds__(256) void gate_quant_vec(const void* __restrict__ x
     }
   }
   const RowScale s = scale_from_amax<MODE>(wave_max(amax));
-  char* qr = (char*)q + row * ldq;
+  char* qr = qd.row(row);
   char* yr = y_out ? (char*)y_out + row * ldy * RC::kES : nullptr;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     if (RC::valid(c, lane, K)) {
       float v[8];
       y.get(c, v);
-      quant_store8<MODE>(qr + RC::col(c, lane), v, s);
+      quant_store8<MODE>(QDst::at(qr, RC::col(c, lane), qd.bs), v, s);
       if (yr) y.store_raw(c, yr + RC::col(c, lane) * RC::kES);
     }
   }
@@ -254,7 +322,7 @@ __global__ __launch_bounds__(256) void gate_quant_vec(const void* __restrict__ x
 template <int MODE, int DT, int NCH, bool FULL, int OUTES>
 __global__ __launch_bounds__(256) void quant_rows_ragged_vec(
     const void* __restrict__ x, int64_t ldx, const SegOffsets segs, int64_t nseg,
-    int64_t width, int64_t K, void* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+    int64_t width, int64_t K, const QDst qd, float* __restrict__ scale,
     int32_t* __restrict__ row_map, void* __restrict__ out, int64_t ldo, int64_t N) {
   const int lane = threadIdx.x & 63;
   const int64_t prow = (int64_t)blockIdx.x * kQuantWaves + (threadIdx.x >> 6);
@@ -277,13 +345,13 @@ __global__ __launch_bounds__(256) void quant_rows_ragged_vec(
   x_.load((const char*)x + prow * ldx * RC::kES, K, lane);
   const RowScale s = scale_from_amax<MODE>(wave_max(x_.amax(K, lane)));
   if constexpr (NCH > 12) x_.fence();  // wide rows: keep them packed between the passes (occupancy)
-  char* qr = (char*)q + dst * ldq;
+  char* qr = qd.row(dst);
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     if (RC::valid(c, lane, K)) {
       float v[8];
       x_.get(c, v);
-      quant_store8<MODE>(qr + RC::col(c, lane), v, s);
+      quant_store8<MODE>(QDst::at(qr, RC::col(c, lane), qd.bs), v, s);
     }
   }
   if (lane == 0) {
@@ -298,18 +366,43 @@ __global__ __launch_bounds__(256) void quant_rows_ragged_vec(
 
 constexpr int64_t kMaxRowBlocks = (int64_t)1 << 30;  // rows per launch of the block-per-row kernels
 
+// The two-row kernel for a K-blocked q (rows of 64-byte pieces 64 bytes apart), in launches of at most
+// kMaxRowBlocks blocks. AMAX_IN: the row amax comes from `amax` (requantization).
+template <int MODE, int DT, bool AMAX_IN>
+hipError_t launch_quant_pair(const void* x, int64_t ldx, const float* amax, int64_t M, int64_t K, QDst q,
+                             float* scale, hipStream_t st) {
+  const int64_t nct = (K / 8 + 127) / 128;  // chunks per thread, K <= kMaxVecK: at most 16
+  for (int64_t r0 = 0; r0 < M; r0 += 2 * kMaxRowBlocks) {
+    const int64_t rows = std::min<int64_t>(M - r0, 2 * kMaxRowBlocks);
+    const char* xr = (const char*)x + r0 * ldx * (DT == kF32 ? 4 : 2);
+    const QDst qr = q.rows_from(r0);
+    const float* ar = AMAX_IN ? amax + r0 : nullptr;
+#define L(N) hipLaunchKernelGGL((quant_rows_pair<MODE, DT, N, AMAX_IN>), dim3((unsigned)((rows + 1) / 2)), dim3(256), 0, st, xr, ldx, ar, rows, K, qr, scale + r0)
+    if (nct <= 1) L(1);
+    else if (nct <= 2) L(2);
+    else if (nct <= 4) L(4);
+    else if (nct <= 6) L(6);
+    else if (nct <= 8) L(8);
+    else if (nct <= 12) L(12);
+    else L(16);
+#undef L
+  }
+  return hipGetLastError();
+}
+
 template <int MODE, int DT>
-hipError_t launch_quant_rows_t(const void* x, int64_t ldx, int64_t M, int64_t K, void* q, int64_t ldq,
-                               float* scale, bool vec, hipStream_t st) {
+hipError_t launch_quant_rows_t(const void* x, int64_t ldx, int64_t M, int64_t K, QDst q, float* scale, bool vec,
+                               hipStream_t st) {
   if (M == 0) return hipSuccess;
+  if (vec && K <= kMaxVecK && q.kblocked()) return launch_quant_pair<MODE, DT, false>(x, ldx, nullptr, M, K, q, scale, st);
   if (vec && K <= kMaxVecK) {
     const int64_t nct = (K / 8 + 255) / 256;
     // one block per row, in launches of at most kMaxRowBlocks rows (the grid's x limit)
     for (int64_t r0 = 0; r0 < M; r0 += kMaxRowBlocks) {
       const unsigned rows = (unsigned)std::min<int64_t>(M - r0, kMaxRowBlocks);
       const char* xr = (const char*)x + r0 * ldx * (DT == kF32 ? 4 : 2);
-      char* qr = (char*)q + r0 * ldq;
-#define L(N) hipLaunchKernelGGL((quant_rows_stream<MODE, DT, N>), dim3(rows), dim3(256), 0, st, xr, ldx, K, qr, ldq, scale + r0)
+      const QDst qr = q.rows_from(r0);
+#define L(N) hipLaunchKernelGGL((quant_rows_stream<MODE, DT, N>), dim3(rows), dim3(256), 0, st, xr, ldx, K, qr, scale + r0)
       if (nct <= 1) L(1);
       else if (nct <= 2) L(2);
       else if (nct <= 4) L(4);
@@ -318,14 +411,14 @@ hipError_t launch_quant_rows_t(const void* x, int64_t ldx, int64_t M, int64_t K,
 #undef L
     }
   } else {
-    hipLaunchKernelGGL((quant_rows_generic<MODE, DT>), quant_grid(M), dim3(256), 0, st, x, ldx, M, K, q, ldq, scale);
+    hipLaunchKernelGGL((quant_rows_generic<MODE, DT>), quant_grid(M), dim3(256), 0, st, x, ldx, M, K, q, scale);
   }
   return hipGetLastError();
 }
 
-hipError_t launch_quant_rows(int mode, int dt, const void* x, int64_t ldx, int64_t M, int64_t K, void* q,
-                             int64_t ldq, float* scale, bool vec, hipStream_t st) {
-#define C(MO, D) if (mode == MO && dt == D) return launch_quant_rows_t<MO, D>(x, ldx, M, K, q, ldq, scale, vec, st)
+hipError_t launch_quant_rows(int mode, int dt, const void* x, int64_t ldx, int64_t M, int64_t K, QDst q,
+                             float* scale, bool vec, hipStream_t st) {
+#define C(MO, D) if (mode == MO && dt == D) return launch_quant_rows_t<MO, D>(x, ldx, M, K, q, scale, vec, st)
   C(kInt8, kBF16); C(kInt8, kF16); C(kInt8, kF32);
   C(kFp8, kBF16); C(kFp8, kF16); C(kFp8, kF32);
 #undef C
@@ -333,15 +426,16 @@ hipError_t launch_quant_rows(int mode, int dt, const void* x, int64_t ldx, int64
 }
 
 template <int MODE, int DT>
-hipError_t launch_quant_rows_amax_t(const void* h, int64_t ldh, const float* amax, int64_t M, int64_t K, void* q,
-                                    int64_t ldq, float* scale, hipStream_t st) {
+hipError_t launch_quant_rows_amax_t(const void* h, int64_t ldh, const float* amax, int64_t M, int64_t K, QDst q,
+                                    float* scale, hipStream_t st) {
   if (M == 0) return hipSuccess;
+  if (q.kblocked()) return launch_quant_pair<MODE, DT, true>(h, ldh, amax, M, K, q, scale, st);
   const int64_t nct = (K / 8 + 255) / 256;  // chunks per thread, K <= kMaxVecK: at most 8
   for (int64_t r0 = 0; r0 < M; r0 += kMaxRowBlocks) {
     const unsigned rows = (unsigned)std::min<int64_t>(M - r0, kMaxRowBlocks);
     const char* hr = (const char*)h + r0 * ldh * (DT == kF32 ? 4 : 2);
-    char* qr = (char*)q + r0 * ldq;
-#define L(N) hipLaunchKernelGGL((quant_rows_amax_stream<MODE, DT, N>), dim3(rows), dim3(256), 0, st, hr, ldh, amax + r0, K, qr, ldq, scale + r0)
+    const QDst qr = q.rows_from(r0);
+#define L(N) hipLaunchKernelGGL((quant_rows_amax_stream<MODE, DT, N>), dim3(rows), dim3(256), 0, st, hr, ldh, amax + r0, K, qr, scale + r0)
     if (nct <= 1) L(1);
     else if (nct <= 2) L(2);
     else if (nct <= 4) L(4);
@@ -353,9 +447,9 @@ hipError_t launch_quant_rows_amax_t(const void* h, int64_t ldh, const float* ama
 }
 
 hipError_t launch_quant_rows_amax(int mode, int dt, const void* h, int64_t ldh, const float* amax, int64_t M,
-                                  int64_t K, void* q, int64_t ldq, float* scale, hipStream_t st) {
+                                  int64_t K, QDst q, float* scale, hipStream_t st) {
   if (K > kMaxVecK) return hipErrorInvalidValue;
-#define C(MO, D) if (mode == MO && dt == D) return launch_quant_rows_amax_t<MO, D>(h, ldh, amax, M, K, q, ldq, scale, st)
+#define C(MO, D) if (mode == MO && dt == D) return launch_quant_rows_amax_t<MO, D>(h, ldh, amax, M, K, q, scale, st)
   C(kInt8, kBF16); C(kInt8, kF16); C(kInt8, kF32);
   C(kFp8, kBF16); C(kFp8, kF16); C(kFp8, kF32);
 #undef C
@@ -364,20 +458,19 @@ hipError_t launch_quant_rows_amax(int mode, int dt, const void* h, int64_t ldh, 
 
 template <int MODE, int DT>
 hipError_t launch_gate_quant_t(const void* x, int64_t ldx, const void* gate, int64_t ldg, int64_t head_dim, int64_t M,
-                               int64_t K, void* q, int64_t ldq, float* scale, void* y_out, int64_t ldy,
-                               hipStream_t st) {
+                               int64_t K, QDst q, float* scale, void* y_out, int64_t ldy, hipStream_t st) {
   if (M == 0) return hipSuccess;
-#define L(N, F) hipLaunchKernelGGL((gate_quant_vec<MODE, DT, N, F>), quant_grid(M), dim3(256), 0, st, x, ldx, gate, ldg, head_dim, M, K, q, ldq, scale, y_out, ldy)
+#define L(N, F) hipLaunchKernelGGL((gate_quant_vec<MODE, DT, N, F>), quant_grid(M), dim3(256), 0, st, x, ldx, gate, ldg, head_dim, M, K, q, scale, y_out, ldy)
   D3_NCH_DISPATCH(K, L);
 #undef L
   return hipGetLastError();
 }
 
 hipError_t launch_gate_quant(int mode, int dt, const void* x, int64_t ldx, const void* gate, int64_t ldg,
-                             int64_t head_dim, int64_t M, int64_t K, void* q, int64_t ldq, float* scale, void* y_out,
+                             int64_t head_dim, int64_t M, int64_t K, QDst q, float* scale, void* y_out,
                              int64_t ldy, hipStream_t st) {
   if (K > kMaxVecK) return hipErrorInvalidValue;
-#define C(MO, D) if (mode == MO && dt == D) return launch_gate_quant_t<MO, D>(x, ldx, gate, ldg, head_dim, M, K, q, ldq, scale, y_out, ldy, st)
+#define C(MO, D) if (mode == MO && dt == D) return launch_gate_quant_t<MO, D>(x, ldx, gate, ldg, head_dim, M, K, q, scale, y_out, ldy, st)
   C(kInt8, kBF16); C(kInt8, kF16); C(kFp8, kBF16); C(kFp8, kF16);
 #undef C
   return hipErrorInvalidValue;
@@ -385,21 +478,21 @@ hipError_t launch_gate_quant(int mode, int dt, const void* x, int64_t ldx, const
 
 template <int MODE, int DT, int OUTES>
 hipError_t launch_quant_ragged_t(const void* x, int64_t ldx, const SegOffsets& segs, int64_t nseg, int64_t width,
-                                 int64_t K, void* q, int64_t ldq, float* scale, int32_t* row_map, void* out,
+                                 int64_t K, QDst q, float* scale, int32_t* row_map, void* out,
                                  int64_t ldo, int64_t N, hipStream_t st) {
   const int64_t rows = nseg * width;
   if (rows == 0) return hipSuccess;
-#define L(NC, F) hipLaunchKernelGGL((quant_rows_ragged_vec<MODE, DT, NC, F, OUTES>), quant_grid(rows), dim3(256), 0, st, x, ldx, segs, nseg, width, K, q, ldq, scale, row_map, out, ldo, N)
+#define L(NC, F) hipLaunchKernelGGL((quant_rows_ragged_vec<MODE, DT, NC, F, OUTES>), quant_grid(rows), dim3(256), 0, st, x, ldx, segs, nseg, width, K, q, scale, row_map, out, ldo, N)
   D3_NCH_DISPATCH(K, L);
 #undef L
   return hipGetLastError();
 }
 
 hipError_t launch_quant_ragged(int mode, int dt, int out_es, const void* x, int64_t ldx, const SegOffsets& segs,
-                               int64_t nseg, int64_t width, int64_t K, void* q, int64_t ldq, float* scale,
+                               int64_t nseg, int64_t width, int64_t K, QDst q, float* scale,
                                int32_t* row_map, void* out, int64_t ldo, int64_t N, hipStream_t st) {
   if (K > kMaxVecK) return hipErrorInvalidValue;
-#define C(MO, D, E) if (mode == MO && dt == D && out_es == E) return launch_quant_ragged_t<MO, D, E>(x, ldx, segs, nseg, width, K, q, ldq, scale, row_map, out, ldo, N, st)
+#define C(MO, D, E) if (mode == MO && dt == D && out_es == E) return launch_quant_ragged_t<MO, D, E>(x, ldx, segs, nseg, width, K, q, scale, row_map, out, ldo, N, st)
   C(kInt8, kBF16, 2); C(kInt8, kBF16, 4); C(kInt8, kF16, 2); C(kInt8, kF16, 4); C(kInt8, kF32, 2); C(kInt8, kF32, 4);
   C(kFp8, kBF16, 2); C(kFp8, kBF16, 4); C(kFp8, kF16, 2); C(kFp8, kF16, 4); C(kFp8, kF32, 2); C(kFp8, kF32, 4);
 #undef C

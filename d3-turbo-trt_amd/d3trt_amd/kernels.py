@@ -63,64 +63,87 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
-def quantize_rows(x: torch.Tensor, mode: str) -> tuple[torch.Tensor, torch.Tensor]:
-    """[M, K] float -> (q [M, K] int8/e4m3fn, scale [M, 1] fp32)."""
+def _qbuf(M: int, K: int, mode: str, device, kblock: bool) -> tuple[torch.Tensor, int, int]:
+    """Output of a quantize call: (q, its ld, the mode code with the layout flag).
+
+    Row-major q is [M, K] (ld K). A K-blocked q (``kblock=True``) is [K // 64, M, 64]: slice b holds
+    bytes 64 b .. 64 b + 63 of every row, rows back to back (ld M, the row capacity). The pipelined
+    GEMM tiles read it as whole 128-byte lines; :func:`gemm` takes either form.
+    """
+    if kblock:
+        if K % 64:
+            raise ValueError(f"a K-blocked q needs K % 64 == 0, got K={K}")
+        return (torch.empty(K // 64, M, 64, dtype=qdtype(mode), device=device), M,
+                mode_code(mode) | _lib.KBLOCK)
+    return torch.empty(M, K, dtype=qdtype(mode), device=device), K, mode_code(mode)
+
+
+def unblock(q: torch.Tensor) -> torch.Tensor:
+    """A K-blocked q [K // 64, M, 64] as the row-major [M, K] it holds (a copy)."""
+    if q.dim() != 3 or q.shape[2] != 64:
+        raise ValueError(f"a K-blocked q is [K // 64, M, 64], got {tuple(q.shape)}")
+    return q.permute(1, 0, 2).reshape(q.shape[1], q.shape[0] * 64)
+
+
+def quantize_rows(x: torch.Tensor, mode: str, *, kblock: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """[M, K] float -> (q [M, K] int8/e4m3fn, scale [M, 1] fp32); q K-blocked with ``kblock``."""
     x = _rows(x, "x")
     M, K = x.shape
-    q = torch.empty(M, K, dtype=qdtype(mode), device=x.device)
+    q, ldq, mc = _qbuf(M, K, mode, x.device, kblock)
     s = torch.empty(M, 1, dtype=torch.float32, device=x.device)
     lib = _lib.load()
-    rc = lib.d3w8a8_quantize_rows(mode_code(mode), dtype_code(x.dtype), x.data_ptr(), x.stride(0), M, K,
-                                  q.data_ptr(), K, s.data_ptr(), _stream(x))
+    rc = lib.d3w8a8_quantize_rows(mc, dtype_code(x.dtype), x.data_ptr(), x.stride(0), M, K,
+                                  q.data_ptr(), ldq, s.data_ptr(), _stream(x))
     _lib.check(rc, "quantize_rows")
     return q, s
 
 
 def rmsnorm_quantize(x: torch.Tensor, weight: torch.Tensor, eps: float, mode: str, *,
                      zero_centered: bool = True, want_normed: bool = False,
-                     clear_amax: Optional[torch.Tensor] = None):
-    """Fused RMSNorm + per-token quant. Returns (q, scale [M,1], normed or None)."""
+                     clear_amax: Optional[torch.Tensor] = None, kblock: bool = False):
+    """Fused RMSNorm + per-token quant. Returns (q, scale [M,1], normed or None); q K-blocked with
+    ``kblock``."""
     x = _rows(x, "x")
     M, K = x.shape
     w = _gpu(weight, "weight").contiguous()
     if w.shape != (K,):
         raise ValueError(f"norm weight shape {tuple(w.shape)} does not match hidden size {K}")
-    q = torch.empty(M, K, dtype=qdtype(mode), device=x.device)
+    q, ldq, mc = _qbuf(M, K, mode, x.device, kblock)
     s = torch.empty(M, 1, dtype=torch.float32, device=x.device)
     normed = torch.empty_like(x, memory_format=torch.contiguous_format) if want_normed else None
     if clear_amax is not None and (clear_amax.numel() < M or clear_amax.dtype != torch.float32):
         raise ValueError("clear_amax must be a float32 buffer of at least M entries")
     lib = _lib.load()
     rc = lib.d3w8a8_rmsnorm_quantize(
-        mode_code(mode), dtype_code(x.dtype), x.data_ptr(), x.stride(0), dtype_code(w.dtype), w.data_ptr(),
-        M, K, float(eps), 1 if zero_centered else 0, q.data_ptr(), K, s.data_ptr(), _ptr(normed),
+        mc, dtype_code(x.dtype), x.data_ptr(), x.stride(0), dtype_code(w.dtype), w.data_ptr(),
+        M, K, float(eps), 1 if zero_centered else 0, q.data_ptr(), ldq, s.data_ptr(), _ptr(normed),
         K if normed is not None else 0, _ptr(clear_amax), _stream(x))
     _lib.check(rc, "rmsnorm_quantize")
     return q, s, normed
 
 
-def quantize_rows_amax(h: torch.Tensor, amax: torch.Tensor, mode: str):
-    """Quantize rows whose amax is already known (SwiGLU output)."""
+def quantize_rows_amax(h: torch.Tensor, amax: torch.Tensor, mode: str, *, kblock: bool = False):
+    """Quantize rows whose amax is already known (SwiGLU output); q K-blocked with ``kblock``."""
     h = _rows(h, "h")
     M, K = h.shape
     if amax.dtype != torch.float32 or amax.numel() < M:
         raise ValueError("amax must be float32 with one entry per row")
-    q = torch.empty(M, K, dtype=qdtype(mode), device=h.device)
+    q, ldq, mc = _qbuf(M, K, mode, h.device, kblock)
     s = torch.empty(M, 1, dtype=torch.float32, device=h.device)
     lib = _lib.load()
-    rc = lib.d3w8a8_quantize_rows_amax(mode_code(mode), dtype_code(h.dtype), h.data_ptr(), h.stride(0),
-                                       amax.data_ptr(), M, K, q.data_ptr(), K, s.data_ptr(), _stream(h))
+    rc = lib.d3w8a8_quantize_rows_amax(mc, dtype_code(h.dtype), h.data_ptr(), h.stride(0),
+                                       amax.data_ptr(), M, K, q.data_ptr(), ldq, s.data_ptr(), _stream(h))
     _lib.check(rc, "quantize_rows_amax")
     return q, s
 
 
 def gate_quantize(x: torch.Tensor, gate: torch.Tensor, mode: str, *, gate_head_dim: int = 0,
-                  want_y: bool = False):
+                  want_y: bool = False, kblock: bool = False):
     """quantize_rows(x * sigmoid(gate)) fused: the o_proj input of a gated attention layer (core.py:297).
 
     ``gate`` is [M, K] (``gate_head_dim=0``), or the q_proj output [M, 2K] whose rows hold per head
     [query (head_dim) | gate (head_dim)] (core.py:231), read in place with ``gate_head_dim=head_dim``.
-    Returns (q [M, K], scale [M, 1], y or None), y = the product in x's dtype.
+    Returns (q [M, K], scale [M, 1], y or None), y = the product in x's dtype; q K-blocked with ``kblock``.
     """
     x = _rows(x, "x")
     gate = _rows(gate, "gate")
@@ -131,22 +154,23 @@ def gate_quantize(x: torch.Tensor, gate: torch.Tensor, mode: str, *, gate_head_d
                          f"(expected [{M}, {want_cols}])")
     if gate.dtype != x.dtype:
         raise ValueError("gate and x must share a dtype")
-    q = torch.empty(M, K, dtype=qdtype(mode), device=x.device)
+    q, ldq, mc = _qbuf(M, K, mode, x.device, kblock)
     s = torch.empty(M, 1, dtype=torch.float32, device=x.device)
     y = torch.empty(M, K, dtype=x.dtype, device=x.device) if want_y else None
     lib = _lib.load()
-    rc = lib.d3w8a8_gate_quantize(mode_code(mode), dtype_code(x.dtype), x.data_ptr(), x.stride(0), gate.data_ptr(),
-                                  gate.stride(0), int(gate_head_dim), M, K, q.data_ptr(), K, s.data_ptr(), _ptr(y),
+    rc = lib.d3w8a8_gate_quantize(mc, dtype_code(x.dtype), x.data_ptr(), x.stride(0), gate.data_ptr(),
+                                  gate.stride(0), int(gate_head_dim), M, K, q.data_ptr(), ldq, s.data_ptr(), _ptr(y),
                                   K if y is not None else 0, _stream(x))
     _lib.check(rc, "gate_quantize")
     return q, s, y
 
 
 def gdn_norm_quantize(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float, head_dim: int,
-                      mode: str, *, want_y: bool = False):
+                      mode: str, *, want_y: bool = False, kblock: bool = False):
     """Qwen3_5RMSNormGated over heads of ``head_dim`` (``delta.norm(core, z)``, core.py:390) fused with the
     per-token quantize of out_proj's input. x, z [M, heads * head_dim]; weight [head_dim].
-    Returns (q [M, K], scale [M, 1], y or None), y = the normed, gated rows in x's dtype."""
+    Returns (q [M, K], scale [M, 1], y or None), y = the normed, gated rows in x's dtype; q K-blocked with
+    ``kblock``."""
     x = _rows(x, "x")
     z = _rows(z, "z")
     M, K = x.shape
@@ -155,26 +179,26 @@ def gdn_norm_quantize(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, ep
     w = _gpu(weight, "weight").contiguous()
     if w.shape != (head_dim,):
         raise ValueError(f"norm weight shape {tuple(w.shape)} does not match head_dim {head_dim}")
-    q = torch.empty(M, K, dtype=qdtype(mode), device=x.device)
+    q, ldq, mc = _qbuf(M, K, mode, x.device, kblock)
     s = torch.empty(M, 1, dtype=torch.float32, device=x.device)
     y = torch.empty(M, K, dtype=x.dtype, device=x.device) if want_y else None
     lib = _lib.load()
-    rc = lib.d3w8a8_gdn_norm_quantize(mode_code(mode), dtype_code(x.dtype), x.data_ptr(), x.stride(0),
+    rc = lib.d3w8a8_gdn_norm_quantize(mc, dtype_code(x.dtype), x.data_ptr(), x.stride(0),
                                       z.data_ptr(), z.stride(0), dtype_code(w.dtype), w.data_ptr(), int(head_dim),
-                                      float(eps), M, K, q.data_ptr(), K, s.data_ptr(), _ptr(y),
+                                      float(eps), M, K, q.data_ptr(), ldq, s.data_ptr(), _ptr(y),
                                       K if y is not None else 0, _stream(x))
     _lib.check(rc, "gdn_norm_quantize")
     return q, s, y
 
 
 def quantize_rows_ragged(x: torch.Tensor, lengths: Sequence[int], mode: str, *,
-                         out: Optional[torch.Tensor] = None):
+                         out: Optional[torch.Tensor] = None, kblock: bool = False):
     """Right-padded [B, W, K] -> packed (q [T, K], scale [T, 1], row_map [T] int32), T = sum(lengths).
 
     The lengths stay on the host: the library folds them into packed-row
     offsets passed to the kernel by value (no host-to-device copy, so the call
     can be captured in a graph). When ``out`` ([B*W, N] view of the final
-    output) is given, its padded rows are zeroed.
+    output) is given, its padded rows are zeroed. With ``kblock`` q is K-blocked, [K // 64, T, 64].
     """
     _gpu(x, "x")
     if x.dim() != 3:
@@ -200,20 +224,20 @@ def quantize_rows_ragged(x: torch.Tensor, lengths: Sequence[int], mode: str, *,
     host_lengths = (ctypes.c_int32 * max(B, 1))(*lengths)
     # at least one row so the pointers are valid when every block is empty (the kernel
     # still runs to zero the padded output rows)
-    q = torch.empty(max(T, 1), K, dtype=qdtype(mode), device=dev)
+    q, ldq, mc = _qbuf(max(T, 1), K, mode, dev, kblock)
     s = torch.empty(max(T, 1), 1, dtype=torch.float32, device=dev)
     row_map = torch.empty(max(T, 1), dtype=torch.int32, device=dev)
     N = out.shape[1] if out is not None else 0
     lib = _lib.load()
     rc = lib.d3w8a8_quantize_rows_ragged(
-        mode_code(mode), dtype_code(x2.dtype), x2.data_ptr(), x2.stride(0), ctypes.addressof(host_lengths), B, W,
-        K, q.data_ptr(), K, s.data_ptr(), row_map.data_ptr(), _ptr(out),
+        mc, dtype_code(x2.dtype), x2.data_ptr(), x2.stride(0), ctypes.addressof(host_lengths), B, W,
+        K, q.data_ptr(), ldq, s.data_ptr(), row_map.data_ptr(), _ptr(out),
         dtype_code(out.dtype) if out is not None else 0, out.stride(0) if out is not None else 0, N,
         _stream(x2))
     _lib.check(rc, "quantize_rows_ragged")
     row_map = row_map[:T]
     row_map.d3_rows = B * W  # output rows the map addresses; gemm() checks its `out` against it
-    return q[:T], s[:T], row_map
+    return (q[:, :T] if kblock else q[:T]), s[:T], row_map
 
 
 def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.Tensor,
@@ -224,6 +248,9 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
          ksplit: int = _lib.KSPLIT_AUTO, noalloc: bool = False) -> torch.Tensor:
     """W8A8 GEMM ``a @ w.T`` with a fused epilogue (see include/d3w8a8.h).
 
+    ``a`` is row-major [M, K] or K-blocked [K // 64, M, 64] (from a quantize call with ``kblock``);
+    the results are the same.
+
     Skinny problems may split K over several workgroups per output tile
     (``ksplit``, automatic by default); the split-K workspace is this module's
     per-(device, stream) buffer from :func:`workspace`. With ``noalloc=True``
@@ -231,10 +258,20 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
     (``d3w8a8_gemm_noalloc``: nothing is allocated for them; such calls on one
     GPU must run in order).
     """
-    a = _rows(a, "a")
+    a_kblk = a.dim() == 3
+    if a_kblk:
+        _gpu(a, "a")
+        if a.shape[2] != 64 or a.stride(2) != 1 or a.stride(1) != 64 or a.stride(0) < 64 * a.shape[1] \
+                or a.stride(0) % 64:
+            raise ValueError(f"a K-blocked a is a [K // 64, M, 64] tensor with rows of 64 contiguous bytes, got "
+                             f"shape {tuple(a.shape)} stride {tuple(a.stride())}")
+        M, K, lda = a.shape[1], 64 * a.shape[0], a.stride(0) // 64
+    else:
+        a = _rows(a, "a")
+        (M, K), lda = a.shape, a.stride(0)
     w = _rows(w, "w")
-    M, K = a.shape
     N = w.shape[0]
+    mc = mode_code(mode) | (_lib.KBLOCK if a_kblk else 0)
     if w.shape[1] != K:
         raise ValueError(f"inner dimensions differ: a {tuple(a.shape)} vs w {tuple(w.shape)}")
     if a.dtype != qdtype(mode) or w.dtype != qdtype(mode):
@@ -283,7 +320,7 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
     st = _stream(a)
     if noalloc:
         rc = lib.d3w8a8_gemm_noalloc(
-            mode_code(mode), a.data_ptr(), a.stride(0), _ptr(a_scale), w.data_ptr(), w.stride(0), _ptr(w_scale),
+            mc, a.data_ptr(), lda, _ptr(a_scale), w.data_ptr(), w.stride(0), _ptr(w_scale),
             M, N, K, epilogue, dtype_code(odt) if epilogue != _lib.EPI_RAW else 0, out.data_ptr(), out.stride(0),
             _ptr(residual), residual.stride(0) if residual is not None else 0, _ptr(row_amax), _ptr(row_map),
             tile, ksplit, st)
@@ -292,13 +329,13 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
     ws = None
     if ksplit != 1:
         # only a plan that splits K touches the workspace (the state-pass shapes never do)
-        need = lib.d3w8a8_gemm_workspace(M, N, K, a.stride(0), w.stride(0), tile, ksplit, WORKSPACE_BYTES)
+        need = lib.d3w8a8_gemm_workspace(M, N, K, K if a_kblk else lda, w.stride(0), tile, ksplit, WORKSPACE_BYTES)
         if need < 0:
             _lib.check(_lib.EINVAL, "gemm")
         if need > 0:
             ws = workspace(a.device, st)
     rc = lib.d3w8a8_gemm_ws(
-        mode_code(mode), a.data_ptr(), a.stride(0), _ptr(a_scale), w.data_ptr(), w.stride(0), _ptr(w_scale),
+        mc, a.data_ptr(), lda, _ptr(a_scale), w.data_ptr(), w.stride(0), _ptr(w_scale),
         M, N, K, epilogue, dtype_code(odt) if epilogue != _lib.EPI_RAW else 0, out.data_ptr(), out.stride(0),
         _ptr(residual), residual.stride(0) if residual is not None else 0, _ptr(row_amax), _ptr(row_map),
         tile, ksplit, _ptr(ws), ws.numel() if ws is not None else 0, st)

@@ -64,18 +64,18 @@ class QuantMLP(nn.Module):
 
     def _swiglu_requant(self, q1: torch.Tensor, s1: torch.Tensor, amax: torch.Tensor):
         gu = self.gate_up_proj
-        M = q1.shape[0]
-        h = torch.empty(M, self.intermediate_size, dtype=self.dtype, device=q1.device)
+        M = s1.shape[0]
+        h = torch.empty(M, self.intermediate_size, dtype=self.dtype, device=s1.device)
         K.gemm(self.mode, q1, s1.reshape(-1), gu.weight, gu.weight_scale, epilogue=_lib.EPI_SWIGLU,
                out_dtype=self.dtype, out=h, row_amax=amax)
-        q2, s2 = K.quantize_rows_amax(h, amax, self.mode)
+        q2, s2 = K.quantize_rows_amax(h, amax, self.mode, kblock=self.down_proj.kblock)
         return h, q2, s2
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """``down(silu(gate) * up)`` of ``x`` (trtllm_stack.py:131-134), [..., H] -> [..., H]."""
         shape = x.shape[:-1]
         flat = x.reshape(-1, self.hidden_size)
-        q1, s1 = K.quantize_rows(flat, self.mode)
+        q1, s1 = K.quantize_rows(flat, self.mode, kblock=self.gate_up_proj.kblock)
         amax = torch.zeros(flat.shape[0], dtype=torch.float32, device=x.device)
         _, q2, s2 = self._swiglu_requant(q1, s1, amax)
         d = self.down_proj
@@ -94,7 +94,7 @@ class QuantMLP(nn.Module):
         M = flat.shape[0]
         amax = torch.empty(M, dtype=torch.float32, device=hidden.device)  # cleared by the norm kernel
         q1, s1, _ = K.rmsnorm_quantize(flat, norm_weight, eps, self.mode, zero_centered=zero_centered,
-                                       clear_amax=amax)
+                                       clear_amax=amax, kblock=self.gate_up_proj.kblock)
         _, q2, s2 = self._swiglu_requant(q1, s1, amax)
         d = self.down_proj
         out = K.gemm(self.mode, q2, s2.reshape(-1), d.weight, d.weight_scale, epilogue=_lib.EPI_RESIDUAL,

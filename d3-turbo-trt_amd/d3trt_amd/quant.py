@@ -88,15 +88,19 @@ def quantize_weight(weight: torch.Tensor, mode: str) -> tuple[torch.Tensor, torc
     return q, s.reshape(-1)
 
 
-def quantize_rows(x: torch.Tensor, mode: str) -> tuple[torch.Tensor, torch.Tensor]:
-    """[M, K] activations -> (quantized [M, K], [M, 1] float32 per-token scale) (quant.py:92-100)."""
+def quantize_rows(x: torch.Tensor, mode: str, *, kblock: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """[M, K] activations -> (quantized [M, K], [M, 1] float32 per-token scale) (quant.py:92-100).
+
+    ``kblock=True`` returns the quantized rows K-blocked, [K // 64, M, 64] (the layout the GEMM tiles
+    load fastest; :func:`d3trt_amd.kernels.unblock` turns it back into [M, K]).
+    """
     if mode not in ("fp8", "int8"):
         # the reference treats every non-fp8 mode as int8 here (quant.py:99-100)
         mode = "int8"
     x2 = x
     if x2.dtype not in (torch.bfloat16, torch.float16, torch.float32):
         x2 = x2.float()
-    return K.quantize_rows(x2, mode)
+    return K.quantize_rows(x2, mode, kblock=kblock)
 
 
 class QuantLinear(nn.Module):
@@ -128,6 +132,9 @@ class QuantLinear(nn.Module):
         self.register_buffer("weight_scale", torch.ones(out_features, dtype=torch.float32, device=device))
         # "hip-i8" / "hip-f8" after the first call
         self.kernel: str | None = None
+        # the activations pass from the quantize kernel to the GEMM K-blocked (whole 128-byte lines per
+        # GEMM load) where K allows it; the result is the same as through row-major rows
+        self.kblock = in_features % 64 == 0
 
     def extra_repr(self) -> str:
         return f"in={self.in_features}, out={self.out_features}, mode={self.mode}"
@@ -151,7 +158,7 @@ class QuantLinear(nn.Module):
         """[..., in] -> [..., out] in ``self.dtype`` (quant.py:148-155): quantize rows, GEMM, dequant."""
         shape = x.shape[:-1]
         flat = x.reshape(-1, self.in_features)
-        q, scale = quantize_rows(flat, self.mode)
+        q, scale = quantize_rows(flat, self.mode, kblock=self.kblock)
         out = K.gemm(self.mode, q, scale.reshape(-1), self.weight, self.weight_scale,
                      epilogue=_lib.EPI_DEQUANT, out_dtype=self.dtype)
         self.kernel = self._kernel_name()
@@ -167,7 +174,7 @@ class QuantLinear(nn.Module):
         shape = x.shape[:-1]
         flat = x.reshape(-1, self.in_features)
         g = gate.reshape(flat.shape[0], -1)
-        q, scale, _ = K.gate_quantize(flat, g, self.mode, gate_head_dim=gate_head_dim)
+        q, scale, _ = K.gate_quantize(flat, g, self.mode, gate_head_dim=gate_head_dim, kblock=self.kblock)
         out = K.gemm(self.mode, q, scale.reshape(-1), self.weight, self.weight_scale,
                      epilogue=_lib.EPI_DEQUANT, out_dtype=self.dtype)
         self.kernel = self._kernel_name()
@@ -180,7 +187,8 @@ class QuantLinear(nn.Module):
         (core.py:390-391; the norm is Qwen3_5RMSNormGated with weight ``norm_weight``)."""
         shape = x.shape[:-1]
         flat = x.reshape(-1, self.in_features)
-        q, scale, _ = K.gdn_norm_quantize(flat, z.reshape(flat.shape), norm_weight, eps, head_dim, self.mode)
+        q, scale, _ = K.gdn_norm_quantize(flat, z.reshape(flat.shape), norm_weight, eps, head_dim, self.mode,
+                                          kblock=self.kblock)
         out = K.gemm(self.mode, q, scale.reshape(-1), self.weight, self.weight_scale,
                      epilogue=_lib.EPI_DEQUANT, out_dtype=self.dtype)
         self.kernel = self._kernel_name()
@@ -197,8 +205,8 @@ class QuantLinear(nn.Module):
         B, W, _ = x.shape
         out = torch.empty(B, W, self.out_features, dtype=self.dtype, device=x.device)
         out2 = out.view(B * W, self.out_features)
-        q, s, row_map = K.quantize_rows_ragged(x, lengths, self.mode, out=out2)
-        if q.shape[0]:
+        q, s, row_map = K.quantize_rows_ragged(x, lengths, self.mode, out=out2, kblock=self.kblock)
+        if row_map.numel():
             K.gemm(self.mode, q, s.reshape(-1), self.weight, self.weight_scale, epilogue=_lib.EPI_DEQUANT,
                    out_dtype=self.dtype, out=out2, row_map=row_map)
         self.kernel = self._kernel_name()

@@ -56,10 +56,10 @@ class StackLayer(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """[M, hidden] bf16 (rows contiguous) -> [M, hidden]."""
         mode = self.qkv_proj.mode
-        q1, s1, _ = K.rmsnorm_quantize(x, self.input_layernorm, self.eps, mode)
+        q1, s1, _ = K.rmsnorm_quantize(x, self.input_layernorm, self.eps, mode, kblock=self.qkv_proj.kblock)
         qkv = K.gemm(mode, q1, s1.reshape(-1), self.qkv_proj.weight, self.qkv_proj.weight_scale,
                      epilogue=_lib.EPI_DEQUANT, out_dtype=x.dtype)
-        q2, s2 = K.quantize_rows(qkv[:, : self.hidden], mode)
+        q2, s2 = K.quantize_rows(qkv[:, : self.hidden], mode, kblock=self.o_proj.kblock)
         h = K.gemm(mode, q2, s2.reshape(-1), self.o_proj.weight, self.o_proj.weight_scale,
                    epilogue=_lib.EPI_RESIDUAL, out_dtype=x.dtype, residual=x)
         return self.mlp.block(h, self.post_attention_layernorm, self.eps)

@@ -35,6 +35,18 @@ extern "C" {
 #define D3W8A8_INT8 0
 #define D3W8A8_FP8 1
 
+/* Layout flag, OR-ed into `mode`: K-blocked quantized activations. Given to a
+ * quantize entry point it sets the layout of q; given to a GEMM entry point,
+ * the layout of a. Byte (m, k) sits at ((k / 64) * ld + m) * 64 + k % 64: each
+ * 64-byte slice of K holds all rows back to back, ld (ldq / lda) is the row
+ * capacity (>= M) and K % 64 == 0. No counterpart in the reference, whose
+ * activations are row-major tensors: it exists for the pipelined GEMM tiles,
+ * which read 64 bytes of K per row per step, half a 128-byte line of each
+ * row when rows are row-major and whole lines when K-blocked. GEMM results
+ * are identical for both layouts. The register-staged tiles (0-2) take
+ * row-major a only; a K-blocked a needs lda < 2^25. */
+#define D3W8A8_KBLOCK 0x100
+
 /* element types of floating-point tensors */
 #define D3W8A8_BF16 0
 #define D3W8A8_F16 1
@@ -73,7 +85,9 @@ const char* d3w8a8_last_error(void);
  * Replaces quant.py:92-100 quantize_rows(x, mode) and, applied to a weight
  * [N, K], quant.py:77-89 quantize_weight (same per-row arithmetic).
  *   x [M, K] (in_dtype, ld ldx) -> q [M, K] int8 / e4m3fn (ld ldq), scale [M] fp32
- *   scale = max(max|x_m|, 1e-12) / (127 | 448); q = clamp(rne(x / scale)) */
+ *   scale = max(max|x_m|, 1e-12) / (127 | 448); q = clamp(rne(x / scale))
+ * Every quantize entry point writes q row-major (ldq >= K) or, with
+ * D3W8A8_KBLOCK in mode, K-blocked (ldq >= rows of q). */
 int d3w8a8_quantize_rows(int mode, int in_dtype, const void* x, int64_t ldx, int64_t M, int64_t K,
                          void* q, int64_t ldq, float* scale, void* stream);
 
@@ -182,7 +196,8 @@ int d3w8a8_gemm_noalloc(int mode, const void* a, int64_t lda, const float* a_sca
                         int ksplit, void* stream);
 
 /* Workspace bytes d3w8a8_gemm_ws uses for this problem, tile and ksplit when
- * given at most `max_bytes` (0 when it would not split); -1 on bad arguments. */
+ * given at most `max_bytes` (0 when it would not split); -1 on bad arguments.
+ * For a K-blocked a, pass lda = K. */
 int64_t d3w8a8_gemm_workspace(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
                               int64_t max_bytes);
 

@@ -184,3 +184,46 @@ def test_split_k_plan_on_the_host():
     header = open(os.path.join(ROOT, "include", "d3w8a8.h")).read()
     assert re.search(r"#define D3W8A8_KSPLIT_AUTO \((-?\d+)\)", header).group(1) == str(_lib.KSPLIT_AUTO)
 
+
+
+def test_kblock_layout_checked_on_the_host():
+    """The K-blocked activation layout (D3W8A8_KBLOCK in mode): its conditions are refused on the host."""
+    import ctypes
+    from d3trt_amd import kernels as K
+    lib = _lib.load()
+    header = open(os.path.join(ROOT, "include", "d3w8a8.h")).read()
+    assert int(re.search(r"#define D3W8A8_KBLOCK (0x[0-9a-fA-F]+)", header).group(1), 16) == _lib.KBLOCK
+    dummy = 256  # never dereferenced: every call below fails in the host-side checks
+    f8k = _lib.FP8 | _lib.KBLOCK
+
+    def gemm(mode, lda, M, K, tile):
+        return lib.d3w8a8_gemm(mode, dummy, lda, dummy, dummy, K, dummy, M, 256, K, 0, 0, dummy, 256, None, 0,
+                               None, None, tile, None)
+
+    assert gemm(f8k, 512, 512, 4096, _lib.TILE_128) == _lib.EINVAL  # register-staged tiles: row-major only
+    assert b"pipelined" in lib.d3w8a8_last_error()
+    assert gemm(f8k, 512, 512, 4096 + 32, -1) == _lib.EINVAL  # K % 64 != 0
+    assert gemm(f8k, 511, 512, 4096, -1) == _lib.EINVAL  # row capacity below M
+    assert gemm(f8k, 1 << 25, 512, 4096, -1) == _lib.EINVAL  # beyond the 32-bit offsets
+    assert b"K-blocked" in lib.d3w8a8_last_error()
+    # row-major rules do not apply to a K-blocked a: lda (the row capacity) may be below K
+    assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, -1, -1, 64 << 20) == 0
+    # quantize entry points: K % 64 and ldq >= rows
+    assert lib.d3w8a8_quantize_rows(f8k, 0, dummy, 96, 4, 96, dummy, 4, dummy, None) == _lib.EINVAL
+    assert b"K % 64" in lib.d3w8a8_last_error()
+    assert lib.d3w8a8_quantize_rows(f8k, 0, dummy, 128, 4, 128, dummy, 3, dummy, None) == _lib.EINVAL
+    assert b"ldq" in lib.d3w8a8_last_error()
+    assert lib.d3w8a8_quantize_rows_amax(f8k, 0, dummy, 128, dummy, 8, 128, dummy, 7, dummy, None) == _lib.EINVAL
+    lens = (ctypes.c_int32 * 2)(3, 5)
+    assert lib.d3w8a8_quantize_rows_ragged(f8k, 0, dummy, 64, ctypes.addressof(lens), 2, 8, 64, dummy, 7, dummy,
+                                           dummy, None, 0, 0, 0, None) == _lib.EINVAL  # 8 packed rows > ldq 7
+    assert b"sum of the lengths" in lib.d3w8a8_last_error()
+    # an unknown flag is an unknown mode
+    assert lib.d3w8a8_quantize_rows(_lib.FP8 | 0x200, 0, dummy, 128, 4, 128, dummy, 128, dummy, None) == _lib.EINVAL
+    # the layout itself: byte (m, k) at ((k // 64) * ld + m) * 64 + k % 64
+    x = torch.arange(5 * 192, dtype=torch.int32).reshape(5, 192)
+    blocked = x.reshape(5, 3, 64).permute(1, 0, 2).contiguous()
+    flat = blocked.reshape(-1)
+    for m, k in ((0, 0), (4, 191), (2, 64), (3, 127)):
+        assert flat[((k // 64) * 5 + m) * 64 + k % 64] == x[m, k]
+    assert torch.equal(K.unblock(blocked), x)

@@ -125,6 +125,7 @@ def test_c4_mlp_block_int8_full_size(dev):
     amax = torch.empty(M, device=dev)
     q1, s1, normed = K.rmsnorm_quantize(xd, norm_w.to(dev), 1e-6, "int8", want_normed=True, clear_amax=amax)
     h, q2, s2 = mlp._swiglu_requant(q1, s1, amax)
+    q2 = K.unblock(q2) if q2.dim() == 3 else q2  # the block hands q2 to down K-blocked
     d = mlp.down_proj
     out2 = K.gemm("int8", q2, s2.view(-1), d.weight, d.weight_scale, epilogue=_lib.EPI_RESIDUAL, residual=xd)
     assert torch.equal(out, out2)
@@ -199,6 +200,7 @@ def test_c5_state_pass_layer_fp8_full_width(dev, c5_stack):
     amax = torch.empty(M, device=dev)
     q3, s3, _ = K.rmsnorm_quantize(xd, layer.post_attention_layernorm, 1e-6, "fp8", clear_amax=amax)
     h, q4, s4 = layer.mlp._swiglu_requant(q3, s3, amax)
+    q4 = K.unblock(q4) if q4.dim() == 3 else q4  # the block hands q4 to down K-blocked
     q3r, s3r = q3.cpu()[rows], s3.cpu()[rows]
     gu = R.dequant(R.fp8_accumulate(q3r, w["wgu_q"]), s3r, w["wgu_s"], torch.bfloat16)
     assert rel_err(h.cpu()[rows], R.swiglu(gu)) < 1e-2
