@@ -33,10 +33,13 @@ int hip_status(hipError_t e, const char* what) {
   return fail(D3W8A8_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-// mode: D3W8A8_INT8 / D3W8A8_FP8, optionally with the D3W8A8_KBLOCK layout flag
-int base_mode(int m) { return m & ~D3W8A8_KBLOCK; }
+// mode: D3W8A8_INT8 / D3W8A8_FP8, optionally with the layout flags D3W8A8_KBLOCK (q / a) and
+// D3W8A8_W_KBLOCK (w of the GEMMs)
+int base_mode(int m) { return m & ~(D3W8A8_KBLOCK | D3W8A8_W_KBLOCK); }
 bool kblk(int m) { return (m & D3W8A8_KBLOCK) != 0; }
+bool w_kblk(int m) { return (m & D3W8A8_W_KBLOCK) != 0; }
 bool mode_ok(int m) { return base_mode(m) == D3W8A8_INT8 || base_mode(m) == D3W8A8_FP8; }
+bool quant_mode_ok(int m) { return mode_ok(m) && !w_kblk(m); }
 
 // Layout of a quantize entry point's q: row-major [rows, K] (ldq >= K; a multiple of 8 where the
 // kernel stores 8 bytes at a time) or, with D3W8A8_KBLOCK, K-blocked (K % 64 == 0, ldq >= rows).
@@ -98,7 +101,7 @@ const char* d3w8a8_last_error(void) { return g_err; }
 
 int d3w8a8_quantize_rows(int mode, int in_dtype, const void* x, int64_t ldx, int64_t M, int64_t K, void* q,
                          int64_t ldq, float* scale, void* stream) {
-  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "quantize_rows: unknown mode %d", mode);
+  if (!quant_mode_ok(mode)) return fail(D3W8A8_EINVAL, "quantize_rows: unknown mode %d", mode);
   if (!dtype_ok(in_dtype)) return fail(D3W8A8_EINVAL, "quantize_rows: unknown dtype %d", in_dtype);
   if (M < 0 || K < 1 || ldx < K) return fail(D3W8A8_EINVAL, "quantize_rows: bad shape M=%lld K=%lld ldx=%lld ldq=%lld", (long long)M, (long long)K, (long long)ldx, (long long)ldq);
   if (const char* e = q_layout_error(mode, M, K, ldq, false)) return fail(D3W8A8_EINVAL, "quantize_rows: %s", e);
@@ -115,7 +118,7 @@ int d3w8a8_quantize_rows(int mode, int in_dtype, const void* x, int64_t ldx, int
 int d3w8a8_rmsnorm_quantize(int mode, int in_dtype, const void* x, int64_t ldx, int w_dtype, const void* w,
                             int64_t M, int64_t K, float eps, int zero_centered, void* q, int64_t ldq, float* scale,
                             void* normed, int64_t ldn, float* clear_amax, void* stream) {
-  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "rmsnorm_quantize: unknown mode %d", mode);
+  if (!quant_mode_ok(mode)) return fail(D3W8A8_EINVAL, "rmsnorm_quantize: unknown mode %d", mode);
   if (!dtype_ok(in_dtype) || !dtype_ok(w_dtype)) return fail(D3W8A8_EINVAL, "rmsnorm_quantize: unknown dtype");
   if (w_dtype != D3W8A8_F32 && w_dtype != in_dtype)
     return fail(D3W8A8_EINVAL, "rmsnorm_quantize: weight dtype must be fp32 or the input dtype");
@@ -137,7 +140,7 @@ int d3w8a8_rmsnorm_quantize(int mode, int in_dtype, const void* x, int64_t ldx, 
 
 int d3w8a8_quantize_rows_amax(int mode, int in_dtype, const void* h, int64_t ldh, const float* amax, int64_t M,
                               int64_t K, void* q, int64_t ldq, float* scale, void* stream) {
-  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "quantize_rows_amax: unknown mode %d", mode);
+  if (!quant_mode_ok(mode)) return fail(D3W8A8_EINVAL, "quantize_rows_amax: unknown mode %d", mode);
   if (!dtype_ok(in_dtype)) return fail(D3W8A8_EINVAL, "quantize_rows_amax: unknown dtype %d", in_dtype);
   if (M < 0 || K < 8 || K % 8 != 0 || K > d3::kMaxVecK || ldh < K)
     return fail(D3W8A8_EINVAL, "quantize_rows_amax: bad shape M=%lld K=%lld", (long long)M, (long long)K);
@@ -155,7 +158,7 @@ int d3w8a8_quantize_rows_amax(int mode, int in_dtype, const void* h, int64_t ldh
 int d3w8a8_gate_quantize(int mode, int in_dtype, const void* x, int64_t ldx, const void* gate, int64_t ldg,
                          int64_t gate_head_dim, int64_t M, int64_t K, void* q, int64_t ldq, float* scale,
                          void* y_out, int64_t ldy, void* stream) {
-  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "gate_quantize: unknown mode %d", mode);
+  if (!quant_mode_ok(mode)) return fail(D3W8A8_EINVAL, "gate_quantize: unknown mode %d", mode);
   if (in_dtype != D3W8A8_BF16 && in_dtype != D3W8A8_F16)
     return fail(D3W8A8_EINVAL, "gate_quantize: inputs must be bf16 or fp16");
   if (M < 0 || K < 8 || K % 8 != 0 || K > d3::kMaxVecK || ldx < K || (y_out && ldy < K))
@@ -179,7 +182,7 @@ int d3w8a8_gate_quantize(int mode, int in_dtype, const void* x, int64_t ldx, con
 int d3w8a8_gdn_norm_quantize(int mode, int in_dtype, const void* x, int64_t ldx, const void* z, int64_t ldz,
                              int w_dtype, const void* w, int64_t head_dim, float eps, int64_t M, int64_t K, void* q,
                              int64_t ldq, float* scale, void* y_out, int64_t ldy, void* stream) {
-  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "gdn_norm_quantize: unknown mode %d", mode);
+  if (!quant_mode_ok(mode)) return fail(D3W8A8_EINVAL, "gdn_norm_quantize: unknown mode %d", mode);
   if (in_dtype != D3W8A8_BF16 && in_dtype != D3W8A8_F16)
     return fail(D3W8A8_EINVAL, "gdn_norm_quantize: inputs must be bf16 or fp16");
   if (w_dtype != in_dtype && w_dtype != D3W8A8_F32)
@@ -203,7 +206,7 @@ int d3w8a8_gdn_norm_quantize(int mode, int in_dtype, const void* x, int64_t ldx,
 int d3w8a8_quantize_rows_ragged(int mode, int in_dtype, const void* x, int64_t ldx, const int32_t* lengths,
                                 int64_t nseg, int64_t width, int64_t K, void* q, int64_t ldq, float* scale,
                                 int32_t* row_map, void* out, int out_dtype, int64_t ldo, int64_t N, void* stream) {
-  if (!mode_ok(mode)) return fail(D3W8A8_EINVAL, "quantize_rows_ragged: unknown mode %d", mode);
+  if (!quant_mode_ok(mode)) return fail(D3W8A8_EINVAL, "quantize_rows_ragged: unknown mode %d", mode);
   if (!dtype_ok(in_dtype) || (out && !dtype_ok(out_dtype)))
     return fail(D3W8A8_EINVAL, "quantize_rows_ragged: unknown dtype");
   if (nseg < 0 || nseg > D3W8A8_MAX_SEGMENTS || width < 0 || K < 8 || K % 8 != 0 || K > d3::kMaxVecK || ldx < K)
@@ -261,9 +264,16 @@ static int gemm_impl(int mode, const void* a, int64_t lda, const float* a_scale,
   } else if (lda < K || lda % 16) {
     return fail(D3W8A8_EINVAL, "gemm: leading dimensions must cover the rows and be multiples of 16");
   }
-  if (ldw < K || ldw % 16 || ldo < ncols)
+  const bool wk = w_kblk(mode);
+  if (wk) {
+    if (K % 64 != 0 || ldw < N || ldw >= d3::kMaxKblkRows)
+      return fail(D3W8A8_EINVAL, "gemm: a K-blocked w needs K %% 64 == 0 and N <= ldw < %lld (ldw: its row capacity)",
+                  (long long)d3::kMaxKblkRows);
+  } else if (ldw < K || ldw % 16) {
     return fail(D3W8A8_EINVAL, "gemm: leading dimensions must cover the rows and be multiples of 16");
-  const d3::GemmPlan plan = d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, workspace_bytes, epilogue, a_kblk);
+  }
+  if (ldo < ncols) return fail(D3W8A8_EINVAL, "gemm: ldo must cover the output row");
+  const d3::GemmPlan plan = d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, workspace_bytes, epilogue, a_kblk, wk);
   if (plan.error) return fail(D3W8A8_EINVAL, "gemm: %s", plan.error);
   if (M == 0 || N == 0) return D3W8A8_OK;
   if (!a || !w || !out || (epilogue != D3W8A8_EPI_RAW && (!a_scale || !w_scale)))
@@ -276,7 +286,7 @@ static int gemm_impl(int mode, const void* a, int64_t lda, const float* a_scale,
   if (epilogue == D3W8A8_EPI_RESIDUAL && (!res || ldr < N)) return fail(D3W8A8_EINVAL, "gemm: residual missing");
   d3::GemmParams p{};
   p.a = (const uint8_t*)a; p.lda = lda; p.a_kblk = a_kblk ? 1 : 0; p.a_scale = a_scale;
-  p.w = (const uint8_t*)w; p.ldw = ldw; p.w_scale = w_scale;
+  p.w = (const uint8_t*)w; p.ldw = ldw; p.w_kblk = wk ? 1 : 0; p.w_scale = w_scale;
   p.M = M; p.N = N; p.K = K;
   p.out = out; p.ldo = ldo; p.res = res; p.ldr = ldr;
   p.row_amax = row_amax; p.row_map = row_map;
@@ -308,10 +318,12 @@ int d3w8a8_gemm_noalloc(int mode, const void* a, int64_t lda, const float* a_sca
                         const float* w_scale, int64_t M, int64_t N, int64_t K, int epilogue, int out_dtype, void* out,
                         int64_t ldo, const void* res, int64_t ldr, float* row_amax, const int32_t* row_map, int tile,
                         int ksplit, void* stream) {
-  if (ksplit > 1 && M > 0 && N > 0 && K > 0 && K % 16 == 0 && (kblk(mode) ? lda >= M : lda >= K) && ldw >= K &&
-      M <= INT32_MAX / 2 && N <= INT32_MAX / 2 && tile >= D3W8A8_TILE_AUTO && tile <= D3W8A8_TILE_WS) {
+  if (ksplit > 1 && M > 0 && N > 0 && K > 0 && K % 16 == 0 && (kblk(mode) ? lda >= M : lda >= K) &&
+      (w_kblk(mode) ? ldw >= N : ldw >= K) && M <= INT32_MAX / 2 && N <= INT32_MAX / 2 &&
+      tile >= D3W8A8_TILE_AUTO && tile <= D3W8A8_TILE_WS) {
     // an explicit split larger than the scratch: name both sizes rather than the generic plan error
-    const d3::GemmPlan want = d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, INT64_MAX, epilogue, kblk(mode));
+    const d3::GemmPlan want =
+        d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, INT64_MAX, epilogue, kblk(mode), w_kblk(mode));
     if (!want.error && want.ws_bytes > kScratchBytes)
       return fail(D3W8A8_EINVAL, "gemm_noalloc: ksplit %d needs %lld bytes of split-K scratch; the library holds %lld",
                   ksplit, (long long)want.ws_bytes, (long long)kScratchBytes);

@@ -83,11 +83,11 @@ TileShape shape_of(int tile) {
 
 constexpr int kMinSplitBytes = 1024;   // bytes of K per split at least
 
-// The DMA kernels address operands as a tile base plus a 32-bit per-lane offset. A K-blocked A keeps
-// its offsets within a tile's rows and two K blocks (lda < kMaxKblkRows, checked by the caller).
-bool dma_offsets_fit(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, bool a_kblk) {
+// The DMA kernels address operands as a tile base plus a 32-bit per-lane offset. A K-blocked operand
+// keeps its offsets within a tile's rows and two K blocks (ld < kMaxKblkRows, checked by the caller).
+bool dma_offsets_fit(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, bool a_kblk, bool w_kblk) {
   const int64_t lim = (int64_t)1 << 32;
-  return (a_kblk || (M - 1) * lda + K < lim) && (N - 1) * ldw + K < lim;
+  return (a_kblk || (M - 1) * lda + K < lim) && (w_kblk || (N - 1) * ldw + K < lim);
 }
 
 // Rounds of tiles the chip runs one after the other (one workgroup per CU).
@@ -161,17 +161,17 @@ int choose_ksplit(int64_t tiles, int nk, int bk, int64_t cus) {
 }  // namespace
 
 GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
-                   int64_t ws_bytes, int epi, bool a_kblk) {
+                   int64_t ws_bytes, int epi, bool a_kblk, bool w_kblk) {
   GemmPlan pl{};
   pl.ksplit = 1;
-  const bool fit = dma_offsets_fit(M, N, K, lda, ldw, a_kblk);
+  const bool fit = dma_offsets_fit(M, N, K, lda, ldw, a_kblk, w_kblk);
   const int64_t cus = device_cu_count();
   pl.tile = tile < 0 ? choose_tile(M, N, K, fit, epi, cus) : tile;
   if (pl.tile >= kTileCount) return pl.error = "unknown tile", pl;
   if (pl.tile == kDma256x192w4 && epi == kEpiSwiGLU)
     return pl.error = "the 256x192 tile has 3 column blocks per wave; SwiGLU needs gate/up pairs", pl;
   const TileShape sh = shape_of(pl.tile);
-  if (a_kblk && !sh.dma) return pl.error = "a K-blocked A needs a pipelined (DMA) tile", pl;
+  if ((a_kblk || w_kblk) && !sh.dma) return pl.error = "a K-blocked operand needs a pipelined (DMA) tile", pl;
   if (sh.dma && K % sh.bk != 0)
     return pl.error = sh.bk == 128 ? "the 128-byte-step tile needs K % 128 == 0" : "the pipelined tiles need K % 64 == 0",
            pl;

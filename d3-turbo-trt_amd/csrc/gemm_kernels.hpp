@@ -368,7 +368,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, ACC (&acc)[TM][TN]
   epilogue<MODE, TM, TN, EPI, OUT, false>(p, acc, wrow0, wcol0, lane, stage, [] {});
 }
 
-// Register-staged tiles: row-major A only (plan_gemm never gives them a K-blocked A).
+// Register-staged tiles: row-major operands only (plan_gemm never gives them a K-blocked one).
 template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
 __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8(GemmParams p) {
   using MF = Mfma<MODE>;
@@ -721,20 +721,21 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   const int lrow = lane & 31, lhalf = lane >> 5;
 
   // DMA sources: uniform tile bases + per-lane 32-bit offsets (the host keeps every operand
-  // offset below 2^32 for this kernel). A is row-major or K-blocked (QDst, kernels.hpp): byte (m, k)
-  // at m * a_rs + (k / 64) * a_bs + k % 64.
+  // offset below 2^32 for this kernel). Each operand is row-major or K-blocked (QDst, kernels.hpp):
+  // byte (m, k) at m * rs + (k / 64) * bs + k % 64.
   const uint8_t* a_base;
   const uint8_t* b_base;
   uint32_t a_off[A_DMA], b_off[B_DMA];
   const int64_t a_rs = p.a_kblk ? 64 : p.lda, a_bs = p.a_kblk ? 64 * p.lda : 64;
-  const int64_t a_step = (BK / 64) * a_bs;  // A bytes per K step
+  const int64_t b_rs = p.w_kblk ? 64 : p.ldw, b_bs = p.w_kblk ? 64 * p.ldw : 64;
+  const int64_t a_step = (BK / 64) * a_bs, b_step = (BK / 64) * b_bs;  // bytes per K step
   auto setup = [&](int t) {
     if constexpr (kSplitTile<BM, BN>) tile_of(t, (int)gridDim.x / S, p.tiles_m, p.tiles_n, tm, tn);
     else tile_of(t, ntiles, p.tiles_m, p.tiles_n, tm, tn);
     m0 = (int64_t)tm * BM;
     n0 = (int64_t)tn * BN;
     a_base = uniform_ptr(p.a + m0 * a_rs + (int64_t)kbeg * a_step);
-    b_base = uniform_ptr(p.w + n0 * p.ldw + (int64_t)kbeg * BK);
+    b_base = uniform_ptr(p.w + n0 * b_rs + (int64_t)kbeg * b_step);
 #pragma unroll
     for (int i = 0; i < A_DMA; ++i) {
       const int row = (i * NW + wave) * RPD + lane / CPR;
@@ -745,7 +746,7 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
     for (int i = 0; i < B_DMA; ++i) {
       const int row = (i * NW + wave) * RPD + lane / CPR;
       const int ch = (lane % CPR) ^ lds_swz<BK>(row);
-      b_off[i] = (uint32_t)((min(n0 + row, p.N - 1) - n0) * p.ldw + ch * 16);
+      b_off[i] = (uint32_t)((min(n0 + row, p.N - 1) - n0) * b_rs + (ch >> 2) * b_bs + (ch & 3) * 16);
     }
   };
   setup(tile);
@@ -756,7 +757,7 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   auto dma_one = [&](auto u_c, auto d_c, int kt) {
     constexpr int U = decltype(u_c)::value % kStages, d = decltype(d_c)::value;
     if constexpr (d < A_DMA) dma16<U * STAGE + d * NW * 1024>(a_base + (int64_t)kt * a_step, a_off[d], lds_wave);
-    else dma16<U * STAGE + A_BYTES + (d - A_DMA) * NW * 1024>(b_base + (int64_t)kt * BK, b_off[d - A_DMA], lds_wave);
+    else dma16<U * STAGE + A_BYTES + (d - A_DMA) * NW * 1024>(b_base + (int64_t)kt * b_step, b_off[d - A_DMA], lds_wave);
   };
   auto dma_stage = [&](auto u_c, int kt) { static_for<0, DPS>([&](auto d_c) { dma_one(u_c, d_c, kt); }); };
 

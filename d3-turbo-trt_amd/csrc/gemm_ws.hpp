@@ -107,16 +107,18 @@ __global__ __launch_bounds__((CW + 1) * 64, 1) void gemm_w8a8_ws(GemmParams p) {
     // ---------------- producer: the weight slab, DW blocks deep ----------------
     // instruction d covers slab rows 8 d .. 8 d + 7: lane j -> row 8 d + j / 8, LDS chunk j % 8 holds
     // logical chunk (j % 8) ^ swz(row); rows past N repeat row N - 1 (their outputs are never stored)
+    // W row-major or K-blocked (QDst, kernels.hpp), as A below
+    const int64_t w_rs = p.w_kblk ? 64 : p.ldw, w_bs = p.w_kblk ? 64 * p.ldw : 64;
     uint32_t w_off[WDMA];
 #pragma unroll
     for (int d = 0; d < WDMA; ++d) {
       const int row = 8 * d + (lane >> 3);
       const int ch = (lane & 7) ^ lds_swz<kWsKB>(row);
-      w_off[d] = (uint32_t)((min(n0 + row, p.N - 1) - n0) * p.ldw + ch * 16);
+      w_off[d] = (uint32_t)((min(n0 + row, p.N - 1) - n0) * w_rs + (ch >> 2) * w_bs + (ch & 3) * 16);
     }
-    const uint8_t* w_slab = p.w + n0 * p.ldw;
+    const uint8_t* w_slab = p.w + n0 * w_rs;
     auto issue_w = [&](int t) {
-      const uint8_t* g = uniform_ptr(w_slab + (int64_t)t * kWsKB);
+      const uint8_t* g = uniform_ptr(w_slab + (int64_t)t * 2 * w_bs);
       const uint32_t slot = lds0 + (uint32_t)(t % DW) * C::WBLK;
       static_for<0, WDMA>([&](auto d_c) {
         constexpr int d = decltype(d_c)::value;

@@ -35,7 +35,8 @@ struct GemmParams {
   int a_kblk;   // A is K-blocked (pipelined tiles only)
   const float* a_scale;
   const uint8_t* w;
-  int64_t ldw;
+  int64_t ldw;  // as lda, for w (w_kblk)
+  int w_kblk;   // W is K-blocked (pipelined tiles only)
   const float* w_scale;
   int64_t M, N, K;
   void* out;
@@ -106,13 +107,13 @@ struct GemmPlan {
   int64_t ws_bytes;  // workspace the plan uses (0 when ksplit == 1)
   const char* error; // non-null: the request is not valid
 };
-// `epi` (an Epilogue) rules out tiles the epilogue cannot use; a K-blocked A (`a_kblk`) rules out the
-// register-staged tiles.
+// `epi` (an Epilogue) rules out tiles the epilogue cannot use; a K-blocked operand (`a_kblk`,
+// `w_kblk`) rules out the register-staged tiles.
 GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
-                   int64_t ws_bytes, int epi, bool a_kblk = false);
+                   int64_t ws_bytes, int epi, bool a_kblk = false, bool w_kblk = false);
 
-// Largest row capacity of a K-blocked A: the pipelined tiles keep per-lane offsets (two K blocks apart
-// at most) below 2^32.
+// Largest row capacity of a K-blocked operand: the pipelined tiles keep per-lane offsets (two K blocks
+// apart at most) below 2^32.
 constexpr int64_t kMaxKblkRows = (int64_t)1 << 25;
 // Launches the plan; p.partial must point to a workspace of plan.ws_bytes.
 hipError_t launch_gemm(int mode, GemmParams p, int epi, int out_dt, const GemmPlan& plan, hipStream_t st);

@@ -19,6 +19,7 @@ INT8, FP8 = 0, 1
 # D3W8A8_KBLOCK, OR-ed into a mode: K-blocked quantized activations (q of the quantize calls, a of
 # the GEMMs): byte (m, k) at ((k // 64) * ld + m) * 64 + k % 64, ld the row capacity
 KBLOCK = 0x100
+W_KBLOCK = 0x200  # D3W8A8_W_KBLOCK: the same layout for the weights of a GEMM
 BF16, F16, F32 = 0, 1, 2
 EPI_DEQUANT, EPI_RAW, EPI_SWIGLU, EPI_RESIDUAL = 0, 1, 2, 3
 TILE_AUTO, TILE_256, TILE_128, TILE_64x128 = -1, 0, 1, 2

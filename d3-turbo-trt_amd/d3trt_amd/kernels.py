@@ -78,6 +78,24 @@ def _qbuf(M: int, K: int, mode: str, device, kblock: bool) -> tuple[torch.Tensor
     return torch.empty(M, K, dtype=qdtype(mode), device=device), K, mode_code(mode)
 
 
+def _kblocked(t: torch.Tensor, name: str) -> tuple[int, int, int]:
+    """(rows, K, row capacity) of a K-blocked operand [K // 64, rows, 64]."""
+    _gpu(t, name)
+    if t.shape[2] != 64 or t.stride(2) != 1 or t.stride(1) != 64 or t.stride(0) < 64 * t.shape[1] \
+            or t.stride(0) % 64:
+        raise ValueError(f"a K-blocked {name} is a [K // 64, rows, 64] tensor with rows of 64 contiguous bytes, "
+                         f"got shape {tuple(t.shape)} stride {tuple(t.stride())}")
+    return t.shape[1], 64 * t.shape[0], t.stride(0) // 64
+
+
+def to_kblock(t: torch.Tensor) -> torch.Tensor:
+    """Row-major [rows, K] (K % 64 == 0) -> K-blocked [K // 64, rows, 64] (a copy)."""
+    rows, K = t.shape
+    if K % 64:
+        raise ValueError(f"K-blocking needs K % 64 == 0, got K={K}")
+    return t.reshape(rows, K // 64, 64).permute(1, 0, 2).contiguous()
+
+
 def unblock(q: torch.Tensor) -> torch.Tensor:
     """A K-blocked q [K // 64, M, 64] as the row-major [M, K] it holds (a copy)."""
     if q.dim() != 3 or q.shape[2] != 64:
@@ -248,8 +266,8 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
          ksplit: int = _lib.KSPLIT_AUTO, noalloc: bool = False) -> torch.Tensor:
     """W8A8 GEMM ``a @ w.T`` with a fused epilogue (see include/d3w8a8.h).
 
-    ``a`` is row-major [M, K] or K-blocked [K // 64, M, 64] (from a quantize call with ``kblock``);
-    the results are the same.
+    ``a`` is row-major [M, K] or K-blocked [K // 64, M, 64] (from a quantize call with ``kblock``), and
+    ``w`` row-major [N, K] or K-blocked [K // 64, N, 64]; the results are the same.
 
     Skinny problems may split K over several workgroups per output tile
     (``ksplit``, automatic by default); the split-K workspace is this module's
@@ -258,21 +276,19 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
     (``d3w8a8_gemm_noalloc``: nothing is allocated for them; such calls on one
     GPU must run in order).
     """
-    a_kblk = a.dim() == 3
+    a_kblk, w_kblk = a.dim() == 3, w.dim() == 3
     if a_kblk:
-        _gpu(a, "a")
-        if a.shape[2] != 64 or a.stride(2) != 1 or a.stride(1) != 64 or a.stride(0) < 64 * a.shape[1] \
-                or a.stride(0) % 64:
-            raise ValueError(f"a K-blocked a is a [K // 64, M, 64] tensor with rows of 64 contiguous bytes, got "
-                             f"shape {tuple(a.shape)} stride {tuple(a.stride())}")
-        M, K, lda = a.shape[1], 64 * a.shape[0], a.stride(0) // 64
+        M, K, lda = _kblocked(a, "a")
     else:
         a = _rows(a, "a")
         (M, K), lda = a.shape, a.stride(0)
-    w = _rows(w, "w")
-    N = w.shape[0]
-    mc = mode_code(mode) | (_lib.KBLOCK if a_kblk else 0)
-    if w.shape[1] != K:
+    if w_kblk:
+        N, Kw, ldw = _kblocked(w, "w")
+    else:
+        w = _rows(w, "w")
+        (N, Kw), ldw = w.shape, w.stride(0)
+    mc = mode_code(mode) | (_lib.KBLOCK if a_kblk else 0) | (_lib.W_KBLOCK if w_kblk else 0)
+    if Kw != K:
         raise ValueError(f"inner dimensions differ: a {tuple(a.shape)} vs w {tuple(w.shape)}")
     if a.dtype != qdtype(mode) or w.dtype != qdtype(mode):
         raise ValueError(f"{mode} GEMM wants {qdtype(mode)} operands, got {a.dtype} and {w.dtype}")
@@ -320,7 +336,7 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
     st = _stream(a)
     if noalloc:
         rc = lib.d3w8a8_gemm_noalloc(
-            mc, a.data_ptr(), lda, _ptr(a_scale), w.data_ptr(), w.stride(0), _ptr(w_scale),
+            mc, a.data_ptr(), lda, _ptr(a_scale), w.data_ptr(), ldw, _ptr(w_scale),
             M, N, K, epilogue, dtype_code(odt) if epilogue != _lib.EPI_RAW else 0, out.data_ptr(), out.stride(0),
             _ptr(residual), residual.stride(0) if residual is not None else 0, _ptr(row_amax), _ptr(row_map),
             tile, ksplit, st)
@@ -329,13 +345,14 @@ def gemm(mode: str, a: torch.Tensor, a_scale: Optional[torch.Tensor], w: torch.T
     ws = None
     if ksplit != 1:
         # only a plan that splits K touches the workspace (the state-pass shapes never do)
-        need = lib.d3w8a8_gemm_workspace(M, N, K, K if a_kblk else lda, w.stride(0), tile, ksplit, WORKSPACE_BYTES)
+        need = lib.d3w8a8_gemm_workspace(M, N, K, K if a_kblk else lda, K if w_kblk else ldw, tile, ksplit,
+                                         WORKSPACE_BYTES)
         if need < 0:
             _lib.check(_lib.EINVAL, "gemm")
         if need > 0:
             ws = workspace(a.device, st)
     rc = lib.d3w8a8_gemm_ws(
-        mc, a.data_ptr(), lda, _ptr(a_scale), w.data_ptr(), w.stride(0), _ptr(w_scale),
+        mc, a.data_ptr(), lda, _ptr(a_scale), w.data_ptr(), ldw, _ptr(w_scale),
         M, N, K, epilogue, dtype_code(odt) if epilogue != _lib.EPI_RAW else 0, out.data_ptr(), out.stride(0),
         _ptr(residual), residual.stride(0) if residual is not None else 0, _ptr(row_amax), _ptr(row_map),
         tile, ksplit, _ptr(ws), ws.numel() if ws is not None else 0, st)

@@ -46,6 +46,11 @@ extern "C" {
  * are identical for both layouts. The register-staged tiles (0-2) take
  * row-major a only; a K-blocked a needs lda < 2^25. */
 #define D3W8A8_KBLOCK 0x100
+/* The same layout for the weights of a GEMM entry point (w, ldw = its row
+ * capacity >= N; K % 64 == 0; ldw < 2^25): OR-ed into `mode` of d3w8a8_gemm,
+ * _gemm_ws and _gemm_noalloc. d3w8a8_quantize_rows with D3W8A8_KBLOCK writes
+ * quantized weights [N, K] in it. */
+#define D3W8A8_W_KBLOCK 0x200
 
 /* element types of floating-point tensors */
 #define D3W8A8_BF16 0
@@ -197,7 +202,7 @@ int d3w8a8_gemm_noalloc(int mode, const void* a, int64_t lda, const float* a_sca
 
 /* Workspace bytes d3w8a8_gemm_ws uses for this problem, tile and ksplit when
  * given at most `max_bytes` (0 when it would not split); -1 on bad arguments.
- * For a K-blocked a, pass lda = K. */
+ * For a K-blocked a or w, pass lda = K or ldw = K. */
 int64_t d3w8a8_gemm_workspace(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
                               int64_t max_bytes);
 

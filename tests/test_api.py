@@ -218,8 +218,17 @@ def test_kblock_layout_checked_on_the_host():
     assert lib.d3w8a8_quantize_rows_ragged(f8k, 0, dummy, 64, ctypes.addressof(lens), 2, 8, 64, dummy, 7, dummy,
                                            dummy, None, 0, 0, 0, None) == _lib.EINVAL  # 8 packed rows > ldq 7
     assert b"sum of the lengths" in lib.d3w8a8_last_error()
-    # an unknown flag is an unknown mode
-    assert lib.d3w8a8_quantize_rows(_lib.FP8 | 0x200, 0, dummy, 128, 4, 128, dummy, 128, dummy, None) == _lib.EINVAL
+    # the weight flag belongs to the GEMMs only; an unknown flag is an unknown mode
+    assert lib.d3w8a8_quantize_rows(_lib.FP8 | _lib.W_KBLOCK, 0, dummy, 128, 4, 128, dummy, 128, dummy,
+                                    None) == _lib.EINVAL
+    assert lib.d3w8a8_quantize_rows(_lib.FP8 | 0x400, 0, dummy, 128, 4, 128, dummy, 128, dummy, None) == _lib.EINVAL
+    assert int(re.search(r"#define D3W8A8_W_KBLOCK (0x[0-9a-fA-F]+)", header).group(1), 16) == _lib.W_KBLOCK
+    f8w = _lib.FP8 | _lib.W_KBLOCK
+    assert lib.d3w8a8_gemm(f8w, dummy, 4096, dummy, dummy, 255, dummy, 512, 256, 4096, 0, 0, dummy, 256, None, 0,
+                           None, None, -1, None) == _lib.EINVAL  # ldw (row capacity) below N
+    assert b"K-blocked w" in lib.d3w8a8_last_error()
+    assert lib.d3w8a8_gemm(f8w, dummy, 4096, dummy, dummy, 256, dummy, 512, 256, 4096, 0, 0, dummy, 256, None, 0,
+                           None, None, _lib.TILE_256, None) == _lib.EINVAL  # register-staged tile
     # the layout itself: byte (m, k) at ((k // 64) * ld + m) * 64 + k % 64
     x = torch.arange(5 * 192, dtype=torch.int32).reshape(5, 192)
     blocked = x.reshape(5, 3, 64).permute(1, 0, 2).contiguous()

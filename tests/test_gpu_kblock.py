@@ -1,11 +1,12 @@
-"""GPU parity of the K-blocked activation layout (D3W8A8_KBLOCK).
+"""GPU parity of the K-blocked operand layout (D3W8A8_KBLOCK for activations, D3W8A8_W_KBLOCK for weights).
 
 K-blocked quantized activations hold byte (m, k) at ((k // 64) * ld + m) * 64 + k % 64: a permutation
 of the row-major bytes. Every quantize entry point must write, K-blocked, exactly the codes and scales
 it writes row-major, and every pipelined GEMM tile must return, from a K-blocked A, exactly what it
 returns from the row-major A (its MFMAs read the same operands in the same K order). The row-major
 paths are pinned against the oracle by the other GPU tests; these chain onto them bit for bit, INT8 and
-FP8 alike, with row capacities above M (ld > M) as well as equal to it.
+FP8 alike, with row capacities above M (ld > M) as well as equal to it. The same holds for K-blocked
+weights, alone and together with K-blocked activations.
 """
 
 from __future__ import annotations
@@ -54,18 +55,23 @@ def test_gemm_kblock_equals_row_major(dev, mode, tile, M, N, Kd):
     s_w = (torch.rand(N, generator=g) * 1e-2 + 1e-4).to(dev)
     res = torch.randn(M, N, generator=g).to(torch.bfloat16).to(dev)
     a_kb = to_kblock(a, cap=M + 3 * (M % 2))
+    w_kb = to_kblock(w, cap=N + 5 * (N % 3 == 0))
+    # K-blocked a, K-blocked w, both
+    variants = ((a_kb, w), (a, w_kb), (a_kb, w_kb))
     print(f"kblock gemm {mode} tile={tile} {M}x{N}x{Kd}", flush=True)
     for epi in (_lib.EPI_RAW, _lib.EPI_DEQUANT, _lib.EPI_RESIDUAL):
         kw = dict(epilogue=epi, tile=tile, residual=res if epi == _lib.EPI_RESIDUAL else None)
         sa, sw = (None, None) if epi == _lib.EPI_RAW else (s_a, s_w)
         ref = K.gemm(mode, a, sa, w, sw, **kw)
-        out = K.gemm(mode, a_kb, sa, w, sw, **kw)
-        assert torch.equal(out, ref), (epi, tile)
+        for v, (av, wv) in enumerate(variants):
+            assert torch.equal(K.gemm(mode, av, sa, wv, sw, **kw), ref), (epi, tile, v)
     if tile != _lib.TILE_DMA_256x192_W4:  # SwiGLU needs gate/up column pairs
-        amax_r, amax_k = torch.zeros(M, device=dev), torch.zeros(M, device=dev)
+        amax_r = torch.zeros(M, device=dev)
         h_r = K.gemm(mode, a, s_a, w, s_w, epilogue=_lib.EPI_SWIGLU, tile=tile, row_amax=amax_r)
-        h_k = K.gemm(mode, a_kb, s_a, w, s_w, epilogue=_lib.EPI_SWIGLU, tile=tile, row_amax=amax_k)
-        assert torch.equal(h_k, h_r) and torch.equal(amax_k, amax_r)
+        for v, (av, wv) in enumerate(variants):
+            amax_k = torch.zeros(M, device=dev)
+            h_k = K.gemm(mode, av, s_a, wv, s_w, epilogue=_lib.EPI_SWIGLU, tile=tile, row_amax=amax_k)
+            assert torch.equal(h_k, h_r) and torch.equal(amax_k, amax_r), v
 
 
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
@@ -76,11 +82,11 @@ def test_split_k_kblock_equals_row_major(dev, mode, tile, ksplit):
     M, N, Kd = 100, 1024, 4096
     a, w = codes(mode, g, M, Kd).to(dev), codes(mode, g, N, Kd).to(dev)
     s_a, s_w = torch.rand(M, generator=g).to(dev), torch.rand(N, generator=g).to(dev)
-    a_kb = to_kblock(a, cap=128)
+    a_kb, w_kb = to_kblock(a, cap=128), to_kblock(w)
     for noalloc in (False, True):
         ref = K.gemm(mode, a, s_a, w, s_w, tile=tile, ksplit=ksplit, noalloc=noalloc)
-        out = K.gemm(mode, a_kb, s_a, w, s_w, tile=tile, ksplit=ksplit, noalloc=noalloc)
-        assert torch.equal(out, ref), noalloc
+        for av, wv in ((a_kb, w), (a, w_kb), (a_kb, w_kb)):
+            assert torch.equal(K.gemm(mode, av, s_a, wv, s_w, tile=tile, ksplit=ksplit, noalloc=noalloc), ref), noalloc
 
 
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
@@ -92,11 +98,12 @@ def test_persistent_walk_kblock_equals_row_major(dev, mode):
     a, w = codes(mode, g, M, Kd).to(dev), codes(mode, g, N, Kd).to(dev)
     s_a, s_w = torch.rand(M, generator=g).to(dev), torch.rand(N, generator=g).to(dev)
     res = torch.randn(M, N, generator=g).to(torch.bfloat16).to(dev)
-    a_kb = to_kblock(a)
+    a_kb, w_kb = to_kblock(a), to_kblock(w)
     for tile in (_lib.TILE_AUTO, _lib.TILE_DMA_256_W4):
         ref = K.gemm(mode, a, s_a, w, s_w, tile=tile, epilogue=_lib.EPI_RESIDUAL, residual=res)
-        out = K.gemm(mode, a_kb, s_a, w, s_w, tile=tile, epilogue=_lib.EPI_RESIDUAL, residual=res)
-        assert torch.equal(out, ref), tile
+        for av, wv in ((a_kb, w), (a_kb, w_kb)):
+            out = K.gemm(mode, av, s_a, wv, s_w, tile=tile, epilogue=_lib.EPI_RESIDUAL, residual=res)
+            assert torch.equal(out, ref), tile
 
 
 QUANT_SHAPES = [(1, 64), (37, 4096), (300, 1024), (129, 12288)]
