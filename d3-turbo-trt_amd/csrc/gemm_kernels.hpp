@@ -674,7 +674,9 @@ struct PersistLayout {
       !kSplitTile<BM, BN> && EPI != kEpiRaw && OUT != kF32 && STAGES + NW * E::BYTES <= kLdsBytes;
 };
 
-template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT, int BK>
+// WALK: the persistent form (one workgroup per CU walking tiles; only where PersistLayout allows it).
+// Otherwise one workgroup per tile, whose epilogue stages its rows in the freed stage memory.
+template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT, int BK, bool WALK>
 __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   using MF = Mfma<MODE>;
   typedef typename MF::frag frag_t;
@@ -699,7 +701,8 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void gemm_w8a8_dma(GemmParams p) {
   static_assert(EPI != kEpiSwiGLU || (TN % 2 == 0), "swiglu needs gate/up block pairs");
   static_assert(SLOTS >= 1, "tile too small for the interleave");
   using PL = PersistLayout<MODE, BM, BN, WM, WN, EPI, OUT, BK>;
-  constexpr bool PERSIST = PL::value;
+  static_assert(!WALK || PL::value, "the persistent form needs room for its epilogue staging");
+  constexpr bool PERSIST = WALK;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages * STAGE + (PERSIST ? NW * PL::E::BYTES : 0)];
 
   const int lane = threadIdx.x & 63;
@@ -944,13 +947,16 @@ static hipError_t launch_dma(GemmParams p, hipStream_t st) {
   p.tiles_m = (int)((p.M + BM - 1) / BM);
   p.tiles_n = (int)((p.N + BN - 1) / BN);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
-  int64_t grid = tiles * p.ksplit;
-  if (PersistLayout<MODE, BM, BN, WM, WN, EPI, OUT, BK>::value && gemm_persistent()) {
+  if constexpr (PersistLayout<MODE, BM, BN, WM, WN, EPI, OUT, BK>::value) {
     // one workgroup per CU; a multiple of the 8 XCDs keeps each workgroup's tiles on its own XCD
     const int64_t cus = device_cu_count() & ~7;
-    if (cus >= 8 && tiles > cus) grid = cus;
+    if (gemm_persistent() && cus >= 8 && tiles > cus) {
+      hipLaunchKernelGGL((gemm_w8a8_dma<MODE, BM, BN, WM, WN, EPI, OUT, BK, true>), dim3((unsigned)cus),
+                         dim3(WM * WN * 64), 0, st, p);
+      return hipGetLastError();
+    }
   }
-  hipLaunchKernelGGL((gemm_w8a8_dma<MODE, BM, BN, WM, WN, EPI, OUT, BK>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((gemm_w8a8_dma<MODE, BM, BN, WM, WN, EPI, OUT, BK, false>), dim3((unsigned)(tiles * p.ksplit)),
                      dim3(WM * WN * 64), 0, st, p);
   if (kSplitTile<BM, BN> && p.ksplit > 1) {
     const hipError_t e = hipGetLastError();

@@ -123,8 +123,8 @@ constexpr int64_t kMaxVecK = 32 * 512;  // longest row the one-pass quant kernel
 // Compute units of the current device (queried once per device).
 int device_cu_count();
 // Whether the pipelined GEMMs that can run persistently (one workgroup per CU
-// walking several tiles) do so: yes, unless D3W8A8_GEMM_PERSIST=0 is set in
-// the environment (read once; a measurement switch).
+// walking several tiles) do so: only with D3W8A8_GEMM_PERSIST=1 in the
+// environment (read at every launch; one workgroup per tile is faster).
 bool gemm_persistent();
 
 // Column slab of the weight-streaming tile: 32 columns, 64 (one gate/up pair) with SwiGLU, and two

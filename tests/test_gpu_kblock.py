@@ -90,9 +90,12 @@ def test_split_k_kblock_equals_row_major(dev, mode, tile, ksplit):
 
 
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
-def test_persistent_walk_kblock_equals_row_major(dev, mode):
-    """More 256x256 tiles than CUs: each workgroup walks several tiles (their prologue DMAs issued inside the
-    previous tile's epilogue)."""
+@pytest.mark.parametrize("walk", ["0", "1"])
+def test_many_tiles_kblock_equals_row_major(dev, mode, walk, monkeypatch):
+    """More 256x256 tiles than CUs, one workgroup per tile and (D3W8A8_GEMM_PERSIST=1) the persistent walk,
+    where each workgroup walks several tiles (their prologue DMAs issued inside the previous tile's
+    epilogue)."""
+    monkeypatch.setenv("D3W8A8_GEMM_PERSIST", walk)
     g = gen(5 + (mode == "fp8"))
     M, N, Kd = 2048 + 100, 8448, 256
     a, w = codes(mode, g, M, Kd).to(dev), codes(mode, g, N, Kd).to(dev)

@@ -1,10 +1,9 @@
-"""GPU parity of the persistent GEMM path.
+"""GPU parity of GEMMs with more output tiles than compute units, in both launch forms.
 
-With more output tiles than compute units, one workgroup per CU walks several
-tiles and issues the next tile's operand DMA inside the current tile's
-epilogue. These shapes have more than 256 tiles and a partial last tile row
-(edge tiles inside the walk); INT8 results are held bit-exact against the
-exact integer product, FP8 to the 1e-2 relative bar.
+One workgroup per tile (the default), and the persistent walk (D3W8A8_GEMM_PERSIST=1): one workgroup
+per CU walks several tiles and issues the next tile's operand DMA inside the current tile's epilogue.
+These shapes have more than 256 tiles and a partial last tile row (edge tiles inside the walk); INT8
+results are held bit-exact against the exact integer product, FP8 to the 1e-2 relative bar.
 """
 
 from __future__ import annotations
@@ -20,6 +19,13 @@ from d3trt_amd import kernels as K
 pytestmark = pytest.mark.gpu
 
 M = 2200  # 9 tile rows of 256, the last one partial
+
+
+@pytest.fixture(params=["0", "1"], ids=["one_tile", "walk"], autouse=True)
+def launch_form(request, monkeypatch):
+    """The library reads D3W8A8_GEMM_PERSIST at every launch."""
+    monkeypatch.setenv("D3W8A8_GEMM_PERSIST", request.param)
+    return request.param
 KD = 256
 
 
