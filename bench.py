@@ -571,6 +571,43 @@ def run_gdn_norm_quant(args):
             "algo_bytes": byts}
 
 
+def run_reference_scaled_mm(args):
+    """The reference's own FP8 GEMM call on this GPU, rowwise torch._scaled_mm(q, w.t(), scale_a [M, 1],
+    scale_b [1, N], out_dtype=bf16) (d3trt/model/quant.py:171-177; hipBLASLt serves it on ROCm), at the
+    four state-pass shapes: weights rotated over > 256 MB (from HBM), back-to-back launches replayed from a
+    HIP graph, median of >= 20 replays. The library GEMM the W8A8 kernels replace, timed like them (its
+    quantize and padding excluded), with the tensorwise form (one scalar scale each) beside it."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    out = {}
+    for name, M, N, Kd in (("qkv", 4096, 6144, 4096), ("o_proj", 4096, 4096, 4096), ("gate_up", 4096, 24576, 4096),
+                           ("down", 4096, 4096, 12288)):
+        a = (torch.randn(M, Kd, generator=gen, device=dev) * 8).to(torch.float8_e4m3fn)
+        n = max(2, -(-ROTATE_BYTES // (N * Kd)))
+        ws = [(torch.randn(N, Kd, generator=gen, device=dev) * 8).to(torch.float8_e4m3fn) for _ in range(n)]
+        sa = torch.rand(M, 1, generator=gen, device=dev) * 1e-3
+        sb = torch.rand(1, N, generator=gen, device=dev) * 1e-3
+        one = torch.ones((), device=dev)
+        ops = 2.0 * M * N * Kd
+        e = {"M": M, "N": N, "K": Kd}
+        for label, (s_a, s_b) in (("rowwise", (sa, sb)), ("tensorwise", (one, one))):
+            try:
+                us = launch_us(lambda i: torch._scaled_mm(a, ws[i % n].t(), scale_a=s_a, scale_b=s_b,
+                                                          out_dtype=torch.bfloat16), 4 * n)
+                e[f"{label}_us"] = round(us, 2)
+                e[f"{label}_frac_peak"] = round(ops / (us * 1e-6) / 1e12 / PEAK_TOPS["fp8"], 4)
+            except (RuntimeError, NotImplementedError) as ex:
+                e[f"{label}_error"] = str(ex)[:200]
+        out[name] = e
+        del ws
+        torch.cuda.empty_cache()
+    out["note"] = ("rowwise = the reference's call (per-token and per-channel scales, bf16 out); tensorwise = "
+                   "one scale per operand, which the reference falls back to where rowwise is missing")
+    return out
+
+
 def run_linear_stack(args):
     """48-layer FP8 projection stack (identity mixer): state pass of 8192 tokens, then 255 question
     blocks of 16 tokens in ragged batches of 8 blocks and of all 255 blocks."""
@@ -889,6 +926,7 @@ def main() -> int:
                  ("mlp_block_int8", run_mlp_block), ("gated_o_proj_quant_fp8", run_gated_quant),
                  ("gdn_norm_quant_fp8", run_gdn_norm_quant),
                  ("question_gemms_fp8_m128", run_question_gemms),
+                 ("reference_scaled_mm_fp8", run_reference_scaled_mm),
                  ("linear_stack_fp8", run_linear_stack))
     if args.config:
         fns = dict(workloads)
