@@ -331,7 +331,7 @@ def run_single_linear(args):
     byts = quant_bytes(M, K) + gemm_bytes(M, N, K)
     cpu = None
     if not args.no_cpu:
-        xc, wq, ws = x.cpu(), lin.weight.cpu(), lin.weight_scale.cpu()
+        xc, wq, ws = x.cpu(), lin.weight_rows().cpu(), lin.weight_scale.cpu()
         cpu = cpu_rate(lambda: R.emulated_linear(xc, wq, ws, "int8", torch.bfloat16), 2.0 * M * N * K, 2.0,
                        "the whole workload: oracle emulated_linear (quant.py:158-162), 128 x 1024 x 1024")
     return {
@@ -373,7 +373,7 @@ def run_ragged(args):
         out["shapes"][f"N{N}"] = {"us": round(us, 2), "tops": round(ops / (us * 1e-6) / 1e12, 1),
                                   "frac_peak": round(ops / (us * 1e-6) / 1e12 / PEAK_TOPS["int8"], 4)}
         if not args.no_cpu:
-            cpu_work.append((lin.weight.cpu(), lin.weight_scale.cpu()))
+            cpu_work.append((lin.weight_rows().cpu(), lin.weight_scale.cpu()))
         del lin
     if cpu_work:
         xb = [x[b, :n].cpu() for b, n in enumerate(lengths[:2])]  # the first two blocks of the batch
@@ -498,9 +498,9 @@ def run_mlp_block(args):
     if not args.no_cpu:
         rows = 32
         xs, nwc = x[:rows].cpu(), nw.cpu()
-        wgu_q = KK.deinterleave_gate_up(gu.weight.view(torch.uint8)).view(gu.weight.dtype).cpu()
+        wgu_q = KK.deinterleave_gate_up(gu.weight_rows().view(torch.uint8)).view(gu.weight.dtype).cpu()
         wgu_s = KK.deinterleave_gate_up(gu.weight_scale).cpu()
-        wd_q, wd_s = dn.weight.cpu(), dn.weight_scale.cpu()
+        wd_q, wd_s = dn.weight_rows().cpu(), dn.weight_scale.cpu()
         cpu = cpu_rate(lambda: R.mlp_block(xs, nwc, 1e-6, wgu_q, wgu_s, wd_q, wd_s, "int8"),
                        total_ops * rows / M, 4.0, f"{rows} of the 4096 rows through the oracle's block "
                        "(norm, quantize, gate_up, SwiGLU, requantize, down, residual)", total_ops)
@@ -657,11 +657,11 @@ def run_linear_stack(args):
         lay = stack.layers[0]
         gu = lay.mlp.gate_up_proj
         w = dict(w_in=lay.input_layernorm.cpu(), w_post=lay.post_attention_layernorm.cpu(),
-                 wqkv_q=lay.qkv_proj.weight.cpu(), wqkv_s=lay.qkv_proj.weight_scale.cpu(),
-                 wo_q=lay.o_proj.weight.cpu(), wo_s=lay.o_proj.weight_scale.cpu(),
-                 wgu_q=KK.deinterleave_gate_up(gu.weight.view(torch.uint8)).view(gu.weight.dtype).cpu(),
+                 wqkv_q=lay.qkv_proj.weight_rows().cpu(), wqkv_s=lay.qkv_proj.weight_scale.cpu(),
+                 wo_q=lay.o_proj.weight_rows().cpu(), wo_s=lay.o_proj.weight_scale.cpu(),
+                 wgu_q=KK.deinterleave_gate_up(gu.weight_rows().view(torch.uint8)).view(gu.weight.dtype).cpu(),
                  wgu_s=KK.deinterleave_gate_up(gu.weight_scale).cpu(),
-                 wd_q=lay.mlp.down_proj.weight.cpu(), wd_s=lay.mlp.down_proj.weight_scale.cpu())
+                 wd_q=lay.mlp.down_proj.weight_rows().cpu(), wd_s=lay.mlp.down_proj.weight_scale.cpu())
         rows = 8
         xs = state[:rows].cpu()
         per_token_layer = 2.0 * 4096 * (6144 + 4096 + 24576) + 2.0 * 12288 * 4096
@@ -841,7 +841,7 @@ def cpu_baseline_state_pass(layers, mode: str, rows: int, seconds: float):
 
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    work = [(x[:rows].cpu(), lin.weight.cpu(), lin.weight_scale.cpu(), N, K) for _, M, N, K, x, lin in layers]
+    work = [(x[:rows].cpu(), lin.weight_rows().cpu(), lin.weight_scale.cpu(), N, K) for _, M, N, K, x, lin in layers]
     ops = sum(2.0 * rows * N * K for _, _, _, N, K in work)
     reps = 0
     t0 = time.perf_counter()

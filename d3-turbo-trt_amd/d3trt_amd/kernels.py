@@ -93,14 +93,16 @@ def to_kblock(t: torch.Tensor) -> torch.Tensor:
     rows, K = t.shape
     if K % 64:
         raise ValueError(f"K-blocking needs K % 64 == 0, got K={K}")
-    return t.reshape(rows, K // 64, 64).permute(1, 0, 2).contiguous()
+    u = t.view(torch.uint8) if t.element_size() == 1 else t  # byte copies for the float8 codes
+    return u.reshape(rows, K // 64, 64).permute(1, 0, 2).contiguous().view(t.dtype)
 
 
 def unblock(q: torch.Tensor) -> torch.Tensor:
     """A K-blocked q [K // 64, M, 64] as the row-major [M, K] it holds (a copy)."""
     if q.dim() != 3 or q.shape[2] != 64:
         raise ValueError(f"a K-blocked q is [K // 64, M, 64], got {tuple(q.shape)}")
-    return q.permute(1, 0, 2).reshape(q.shape[1], q.shape[0] * 64)
+    u = q.view(torch.uint8) if q.element_size() == 1 else q
+    return u.permute(1, 0, 2).reshape(q.shape[1], q.shape[0] * 64).view(q.dtype)
 
 
 def quantize_rows(x: torch.Tensor, mode: str, *, kblock: bool = False) -> tuple[torch.Tensor, torch.Tensor]:

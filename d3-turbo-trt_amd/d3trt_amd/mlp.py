@@ -58,7 +58,7 @@ class QuantMLP(nn.Module):
                 f"gate_up shape mismatch: module {(gu.out_features, gu.in_features)} vs {tuple(gate_up.shape)}"
             )
         q, s = quantize_weight(gate_up.to(gu.weight.device), self.mode)
-        gu.weight.copy_(K.interleave_gate_up(q.view(torch.uint8)).view(q.dtype))
+        gu.set_weight_rows(K.interleave_gate_up(q.view(torch.uint8)).view(q.dtype))
         gu.weight_scale.copy_(K.interleave_gate_up(s))
         self.down_proj.load_full(down)
 

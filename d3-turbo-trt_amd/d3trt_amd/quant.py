@@ -73,19 +73,38 @@ def quantizable(in_features: int, out_features: int) -> bool:
     return in_features % 16 == 0 and out_features % 16 == 0
 
 
-def quantize_weight(weight: torch.Tensor, mode: str) -> tuple[torch.Tensor, torch.Tensor]:
+def quantize_weight(weight: torch.Tensor, mode: str, *, kblock: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
     """[N, K] float -> ([N, K] fp8/int8, [N] float32 per-channel scale) (quant.py:77-89).
 
     Per output channel: scale = max(max|w_n|, 1e-12) / 127 (or / 448); the
-    quantization is the same per-row kernel as :func:`quantize_rows`.
+    quantization is the same per-row kernel as :func:`quantize_rows`. ``kblock=True`` returns the
+    codes K-blocked, [K // 64, N, 64] (QuantLinear's storage).
     """
     if mode not in ("fp8", "int8"):
         raise ValueError(f"cannot quantize weights to {mode!r}")
     w = weight
     if w.dtype not in (torch.bfloat16, torch.float16, torch.float32):
         w = w.float()
-    q, s = K.quantize_rows(w, mode)
+    q, s = K.quantize_rows(w, mode, kblock=kblock)
     return q, s.reshape(-1)
+
+
+def _weight_rows_in_state_dict(module: "QuantLinear", state_dict: dict, prefix: str, local_metadata: dict):
+    """state_dict() hook: a K-blocked weight leaves as the reference's row-major [out, in]."""
+    key = prefix + "weight"
+    if module.weight_kblock and key in state_dict:
+        state_dict[key] = K.unblock(state_dict[key])
+    return state_dict
+
+
+def _weight_from_state_dict(module: "QuantLinear", state_dict: dict, prefix: str, local_metadata: dict,
+                            strict: bool, missing_keys: list, unexpected_keys: list, error_msgs: list) -> None:
+    """load_state_dict() pre-hook: a row-major [out, in] weight is K-blocked into the module's storage."""
+    key = prefix + "weight"
+    w = state_dict.get(key)
+    if module.weight_kblock and isinstance(w, torch.Tensor) and tuple(w.shape) == (module.out_features,
+                                                                                   module.in_features):
+        state_dict[key] = K.to_kblock(w)
 
 
 def quantize_rows(x: torch.Tensor, mode: str, *, kblock: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
@@ -126,10 +145,16 @@ class QuantLinear(nn.Module):
         self.dtype = dtype
         self.tp_size = 1
         storage = _FP8 if mode == "fp8" else torch.int8
-        self.register_buffer(
-            "weight", torch.empty(out_features, in_features, dtype=storage, device=device)
-        )
+        # The weight codes are stored the way the GEMM loads them fastest: K-blocked,
+        # [in // 64, out, 64] with byte (n, k) at ((k // 64) * out + n) * 64 + k % 64, where in % 64 == 0
+        # (row-major [out, in] otherwise). state_dict() and load_state_dict() exchange the reference's
+        # [out, in]; weight_rows() / set_weight_rows() read and write that form.
+        self.weight_kblock = in_features % 64 == 0
+        wshape = (in_features // 64, out_features, 64) if self.weight_kblock else (out_features, in_features)
+        self.register_buffer("weight", torch.empty(*wshape, dtype=storage, device=device))
         self.register_buffer("weight_scale", torch.ones(out_features, dtype=torch.float32, device=device))
+        self._register_state_dict_hook(_weight_rows_in_state_dict)
+        self._register_load_state_dict_pre_hook(_weight_from_state_dict, with_module=True)
         # "hip-i8" / "hip-f8" after the first call
         self.kernel: str | None = None
         # the activations pass from the quantize kernel to the GEMM K-blocked (whole 128-byte lines per
@@ -139,6 +164,19 @@ class QuantLinear(nn.Module):
     def extra_repr(self) -> str:
         return f"in={self.in_features}, out={self.out_features}, mode={self.mode}"
 
+    def weight_rows(self) -> torch.Tensor:
+        """The weight codes as the reference holds them, row-major [out, in] (a copy when K-blocked)."""
+        return K.unblock(self.weight) if self.weight_kblock else self.weight
+
+    @torch.no_grad()
+    def set_weight_rows(self, q: torch.Tensor) -> None:
+        """Store row-major [out, in] weight codes (the reference's layout) into the weight buffer."""
+        if tuple(q.shape) != (self.out_features, self.in_features) or q.dtype != self.weight.dtype:
+            raise ValueError(f"weight codes must be {self.weight.dtype} [{self.out_features}, {self.in_features}], "
+                             f"got {q.dtype} {tuple(q.shape)}")
+        q = q.to(self.weight.device)
+        self.weight.copy_(K.to_kblock(q) if self.weight_kblock else q)
+
     @torch.no_grad()
     def load_full(self, full: torch.Tensor) -> None:
         """Quantize a full-precision [out, in] weight into the buffers (quant.py:137-146)."""
@@ -147,7 +185,7 @@ class QuantLinear(nn.Module):
                 f"linear shape mismatch: module {(self.out_features, self.in_features)} "
                 f"vs checkpoint {tuple(full.shape)}"
             )
-        q, scale = quantize_weight(full.to(self.weight.device), self.mode)
+        q, scale = quantize_weight(full.to(self.weight.device), self.mode, kblock=self.weight_kblock)
         self.weight.copy_(q)
         self.weight_scale.copy_(scale)
 

@@ -32,7 +32,7 @@ GATE_UP_LAYOUT = "interleaved-32"  # kernels.interleave_gate_up
 
 
 def _linear_tensors(prefix: str, lin: QuantLinear, out: dict) -> None:
-    out[f"{prefix}.weight"] = lin.weight.detach().contiguous().cpu()
+    out[f"{prefix}.weight"] = lin.weight_rows().detach().contiguous().cpu()  # [out, in], row-major
     out[f"{prefix}.weight_scale"] = lin.weight_scale.detach().contiguous().cpu()
 
 
@@ -63,13 +63,13 @@ def save_quantized(path: str, modules: Mapping[str, nn.Module | torch.Tensor]) -
 def _fill(lin: QuantLinear, handle: Any, prefix: str) -> None:
     w = handle.get_tensor(f"{prefix}.weight")
     s = handle.get_tensor(f"{prefix}.weight_scale")
-    if w.dtype != lin.weight.dtype or tuple(w.shape) != tuple(lin.weight.shape):
+    if w.dtype != lin.weight.dtype or tuple(w.shape) != (lin.out_features, lin.in_features):
         raise ValueError(f"{prefix}.weight: file has {w.dtype} {tuple(w.shape)}, module wants "
-                         f"{lin.weight.dtype} {tuple(lin.weight.shape)}")
+                         f"{lin.weight.dtype} {(lin.out_features, lin.in_features)}")
     if s.dtype != torch.float32 or tuple(s.shape) != tuple(lin.weight_scale.shape):
         raise ValueError(f"{prefix}.weight_scale: file has {s.dtype} {tuple(s.shape)}")
     with torch.no_grad():
-        lin.weight.copy_(w)
+        lin.set_weight_rows(w)
         lin.weight_scale.copy_(s)
 
 

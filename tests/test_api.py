@@ -50,7 +50,9 @@ def test_constructor_errors_and_buffers():
     with pytest.raises(ValueError):
         quant.QuantLinear(64, 32, mode="none", dtype=torch.bfloat16, device="cpu")
     layer = quant.QuantLinear(64, 32, mode="fp8", dtype=torch.bfloat16, device="cpu")
-    assert layer.weight.dtype == torch.float8_e4m3fn and layer.weight.shape == (32, 64)
+    assert layer.weight.dtype == torch.float8_e4m3fn and layer.weight_rows().shape == (32, 64)
+    # stored K-blocked ([in / 64, out, 64]); the state dict carries the reference's [out, in]
+    assert layer.weight.shape == (1, 32, 64) and layer.state_dict()["weight"].shape == (32, 64)
     assert layer.weight_scale.dtype == torch.float32 and torch.all(layer.weight_scale == 1)
     assert layer.tp_size == 1 and layer.kernel is None
     assert "weight" in dict(layer.named_buffers()) and "weight_scale" in dict(layer.named_buffers())
@@ -236,3 +238,24 @@ def test_kblock_layout_checked_on_the_host():
     for m, k in ((0, 0), (4, 191), (2, 64), (3, 127)):
         assert flat[((k // 64) * 5 + m) * 64 + k % 64] == x[m, k]
     assert torch.equal(K.unblock(blocked), x)
+
+
+def test_weight_storage_and_state_dict_on_the_host():
+    """QuantLinear stores its codes K-blocked where in % 64 == 0; weight_rows(), state_dict() and
+    load_state_dict() exchange the reference's row-major [out, in] codes."""
+    g = torch.Generator().manual_seed(3)
+    lin = quant.QuantLinear(128, 48, mode="int8", dtype=torch.bfloat16, device="cpu")
+    q = torch.randint(-127, 128, (48, 128), generator=g, dtype=torch.int16).to(torch.int8)
+    lin.set_weight_rows(q)
+    assert lin.weight.shape == (2, 48, 64) and torch.equal(lin.weight_rows(), q)
+    assert torch.equal(lin.weight[1, 5], q[5, 64:])  # byte (n, k) at ((k // 64) * out + n) * 64 + k % 64
+    sd = lin.state_dict()
+    assert torch.equal(sd["weight"], q) and torch.equal(lin.weight_rows(), q)  # the buffer is untouched
+    other = quant.QuantLinear(128, 48, mode="int8", dtype=torch.bfloat16, device="cpu")
+    other.load_state_dict(sd)
+    assert torch.equal(other.weight, lin.weight)
+    with pytest.raises(ValueError):
+        lin.set_weight_rows(q[:, :64])
+    # K not a multiple of 64: row-major storage
+    narrow = quant.QuantLinear(80, 16, mode="int8", dtype=torch.bfloat16, device="cpu")
+    assert narrow.weight.shape == (16, 80) and narrow.state_dict()["weight"].shape == (16, 80)

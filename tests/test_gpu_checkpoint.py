@@ -34,15 +34,15 @@ def test_streamed_weights_equal_oracle_quantization(dev, tmp_path, mode):
     for i, layer in enumerate(st.layers):
         n = layer_names(i)
         wq, ws = R.quantize_weight(torch.cat([tensors[n["q_proj"]], tensors[n["k_proj"]], tensors[n["v_proj"]]]), mode)
-        assert _same(layer.qkv_proj.weight.cpu(), wq) and torch.equal(layer.qkv_proj.weight_scale.cpu(), ws)
+        assert _same(layer.qkv_proj.weight_rows().cpu(), wq) and torch.equal(layer.qkv_proj.weight_scale.cpu(), ws)
         wq, ws = R.quantize_weight(tensors[n["o_proj"]], mode)
-        assert _same(layer.o_proj.weight.cpu(), wq) and torch.equal(layer.o_proj.weight_scale.cpu(), ws)
+        assert _same(layer.o_proj.weight_rows().cpu(), wq) and torch.equal(layer.o_proj.weight_scale.cpu(), ws)
         wq, ws = R.quantize_weight(torch.cat([tensors[n["gate_proj"]], tensors[n["up_proj"]]]), mode)
         gu = layer.mlp.gate_up_proj
-        assert _same(K.deinterleave_gate_up(gu.weight.view(torch.uint8)).cpu(), wq)
+        assert _same(K.deinterleave_gate_up(gu.weight_rows().view(torch.uint8)).cpu(), wq)
         assert torch.equal(K.deinterleave_gate_up(gu.weight_scale).cpu(), ws)
         wq, ws = R.quantize_weight(tensors[n["down_proj"]], mode)
-        assert _same(layer.mlp.down_proj.weight.cpu(), wq)
+        assert _same(layer.mlp.down_proj.weight_rows().cpu(), wq)
         assert torch.equal(layer.mlp.down_proj.weight_scale.cpu(), ws)
         assert torch.equal(layer.input_layernorm.cpu(), tensors[n["input_layernorm"]])
         assert torch.equal(layer.post_attention_layernorm.cpu(), tensors[n["post_attention_layernorm"]])

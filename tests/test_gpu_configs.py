@@ -48,7 +48,7 @@ def test_c1_single_int8_linear_seed0_equals_reference_cpu_path(dev):
     wq_ref, ws_ref = R.quantize_weight(w, "int8")
     lin = QuantLinear(Kd, N, mode="int8", dtype=torch.bfloat16, device=dev)
     lin.load_full(w.to(dev))
-    assert torch.equal(lin.weight.cpu(), wq_ref) and torch.equal(lin.weight_scale.cpu(), ws_ref)
+    assert torch.equal(lin.weight_rows().cpu(), wq_ref) and torch.equal(lin.weight_scale.cpu(), ws_ref)
     out = lin(x.to(dev)).cpu()
     assert lin.kernel == "hip-i8"
     ref = R.emulated_linear(x, wq_ref, ws_ref, "int8", torch.bfloat16)
@@ -163,11 +163,11 @@ def test_c4_mlp_block_int8_full_size(dev):
 def _oracle_layer_weights(layer):
     gu = layer.mlp.gate_up_proj
     return dict(w_in=layer.input_layernorm.cpu(), w_post=layer.post_attention_layernorm.cpu(),
-                wqkv_q=layer.qkv_proj.weight.cpu(), wqkv_s=layer.qkv_proj.weight_scale.cpu(),
-                wo_q=layer.o_proj.weight.cpu(), wo_s=layer.o_proj.weight_scale.cpu(),
-                wgu_q=K.deinterleave_gate_up(gu.weight.view(torch.uint8)).view(gu.weight.dtype).cpu(),
+                wqkv_q=layer.qkv_proj.weight_rows().cpu(), wqkv_s=layer.qkv_proj.weight_scale.cpu(),
+                wo_q=layer.o_proj.weight_rows().cpu(), wo_s=layer.o_proj.weight_scale.cpu(),
+                wgu_q=K.deinterleave_gate_up(gu.weight_rows().view(torch.uint8)).view(gu.weight.dtype).cpu(),
                 wgu_s=K.deinterleave_gate_up(gu.weight_scale).cpu(),
-                wd_q=layer.mlp.down_proj.weight.cpu(), wd_s=layer.mlp.down_proj.weight_scale.cpu())
+                wd_q=layer.mlp.down_proj.weight_rows().cpu(), wd_s=layer.mlp.down_proj.weight_scale.cpu())
 
 
 @pytest.fixture(scope="module")

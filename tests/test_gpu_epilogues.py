@@ -124,7 +124,7 @@ def test_ragged_equals_separate_blocks(dev, mode):
         x[b, :n] = R.outlier_activations(g, n, Kd)
     wq, ws = R.quantize_weight(R.gaussian_weight(g, N, Kd), mode)
     lin = QuantLinear(Kd, N, mode=mode, dtype=torch.bfloat16, device=dev)
-    lin.weight.copy_(wq.to(dev))
+    lin.set_weight_rows(wq.to(dev))
     lin.weight_scale.copy_(ws.to(dev))
     xd = x.to(dev)
     out = lin.forward_ragged(xd, lengths).cpu()
@@ -156,7 +156,7 @@ def test_ragged_with_empty_blocks(dev):
             x[b, :n] = R.outlier_activations(g, n, Kd)
     wq, ws = R.quantize_weight(R.gaussian_weight(g, N, Kd), "int8")
     lin = QuantLinear(Kd, N, mode="int8", dtype=torch.bfloat16, device=dev)
-    lin.weight.copy_(wq.to(dev))
+    lin.set_weight_rows(wq.to(dev))
     lin.weight_scale.copy_(ws.to(dev))
     out = lin.forward_ragged(x.to(dev), lengths).cpu()
     for b, n in enumerate(lengths):

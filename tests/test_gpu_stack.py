@@ -25,12 +25,12 @@ def _stack(dev, layers, mode, seed):
 def _oracle_weights(layer, mode):
     """Quantized weights of one layer in the oracle's layout (gate_up back in [gate; up] order)."""
     gu = layer.mlp.gate_up_proj
-    wgu_q = K.deinterleave_gate_up(gu.weight.view(torch.uint8)).view(gu.weight.dtype).cpu()
+    wgu_q = K.deinterleave_gate_up(gu.weight_rows().view(torch.uint8)).view(gu.weight.dtype).cpu()
     wgu_s = K.deinterleave_gate_up(gu.weight_scale).cpu()
     return dict(w_in=layer.input_layernorm.cpu(), w_post=layer.post_attention_layernorm.cpu(),
-                wqkv_q=layer.qkv_proj.weight.cpu(), wqkv_s=layer.qkv_proj.weight_scale.cpu(),
-                wo_q=layer.o_proj.weight.cpu(), wo_s=layer.o_proj.weight_scale.cpu(),
-                wgu_q=wgu_q, wgu_s=wgu_s, wd_q=layer.mlp.down_proj.weight.cpu(),
+                wqkv_q=layer.qkv_proj.weight_rows().cpu(), wqkv_s=layer.qkv_proj.weight_scale.cpu(),
+                wo_q=layer.o_proj.weight_rows().cpu(), wo_s=layer.o_proj.weight_scale.cpu(),
+                wgu_q=wgu_q, wgu_s=wgu_s, wd_q=layer.mlp.down_proj.weight_rows().cpu(),
                 wd_s=layer.mlp.down_proj.weight_scale.cpu())
 
 

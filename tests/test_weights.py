@@ -18,7 +18,7 @@ def _linear(mode, n, k, seed):
     lin = QuantLinear(k, n, mode=mode, dtype=torch.bfloat16, device="cpu")
     q, s = R.quantize_weight(R.gaussian_weight(gen(seed), n, k), mode)
     with torch.no_grad():
-        lin.weight.copy_(q)
+        lin.set_weight_rows(q)
         lin.weight_scale.copy_(s)
     return lin
 
@@ -29,9 +29,9 @@ def _mlp(mode, h, i, seed):
     gu_q, gu_s = R.quantize_weight(torch.cat([R.gaussian_weight(g, i, h), R.gaussian_weight(g, i, h)]), mode)
     d_q, d_s = R.quantize_weight(R.gaussian_weight(g, h, i), mode)
     with torch.no_grad():
-        mlp.gate_up_proj.weight.copy_(K.interleave_gate_up(gu_q.view(torch.uint8)).view(gu_q.dtype))
+        mlp.gate_up_proj.set_weight_rows(K.interleave_gate_up(gu_q.view(torch.uint8)).view(gu_q.dtype))
         mlp.gate_up_proj.weight_scale.copy_(K.interleave_gate_up(gu_s))
-        mlp.down_proj.weight.copy_(d_q)
+        mlp.down_proj.set_weight_rows(d_q)
         mlp.down_proj.weight_scale.copy_(d_s)
     return mlp
 
