@@ -97,6 +97,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
         // y, rounded to DT, kept packed (the normed output is stored from these words as they are)
         RC y;
         float amax = 0.0f;
+        [[maybe_unused]] Bf16PairAmax am16;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
           if (RC::valid(c, lane, K)) {
@@ -110,11 +111,16 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_vec(
               float p0 = v[i] * rstd, p1 = v[i + 1] * rstd;
               p0 = p0 * g[i];
               p1 = p1 * g[i + 1];
-              y.put_pair(c, i / 2, p0, p1);
-              amax = amax_acc(amax_acc(amax, p0), p1);
+              if constexpr (DT == kBF16) {
+                am16.add(y.put_pair_bits(c, i / 2, p0, p1));
+              } else {
+                y.put_pair(c, i / 2, p0, p1);
+                amax = amax_acc(amax_acc(amax, p0), p1);
+              }
             }
           }
         }
+        if constexpr (DT == kBF16) amax = am16.value();
         const RowScale s = scale_from_amax<MODE>(wave_max(amax));
         if constexpr (NCH > 12) y.fence();  // wide rows: keep y packed between the passes (registers)
         char* qr = qd.row(row);
@@ -194,6 +200,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_rowblock(
   // y, rounded to DT and kept packed
   RC y[NCT];
   float amax = 0.0f;
+  [[maybe_unused]] Bf16PairAmax am16;
 #pragma unroll
   for (int i = 0; i < NCT; ++i) {
     if (t + 256 * i < nch) {
@@ -206,11 +213,16 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_rowblock(
         float p0 = v[k] * rstd, p1 = v[k + 1] * rstd;
         p0 = p0 * g0;
         p1 = p1 * g1;
-        y[i].put_pair(0, k / 2, p0, p1);
-        amax = amax_acc(amax_acc(amax, p0), p1);
+        if constexpr (DT == kBF16) {
+          am16.add(y[i].put_pair_bits(0, k / 2, p0, p1));
+        } else {
+          y[i].put_pair(0, k / 2, p0, p1);
+          amax = amax_acc(amax_acc(amax, p0), p1);
+        }
       }
     }
   }
+  if constexpr (DT == kBF16) amax = am16.value();
   amax = wave_max(amax);
   if (lane == 0) red[1][wave] = amax;
   __syncthreads();

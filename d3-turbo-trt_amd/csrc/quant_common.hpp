@@ -27,6 +27,21 @@ __device__ __forceinline__ float dot2_sq(uint32_t w, float acc) {
   }
 }
 
+// Running max of magnitudes over packed bf16 pairs. With the sign bits cleared, the two 16-bit halves
+// order like the values (NaN above inf) as unsigned integers, so one AND and one packed 16-bit max per
+// pair give what amax_acc gives after unpacking both to fp32 (three ops and the two unpacks): the bf16
+// magnitude shifted into the high half is the fp32 bit pattern of the same value.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+struct Bf16PairAmax {
+  u16x2 m = {0, 0};
+  __device__ __forceinline__ void add(uint32_t w) {
+    m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w & 0x7fff7fffu));
+  }
+  __device__ __forceinline__ float value() const {
+    return __uint_as_float((uint32_t)(m.x > m.y ? m.x : m.y) << 16);
+  }
+};
+
 // One row of a [*, K] tensor held by one wave: lane l owns the 8-element
 // chunks at columns 512 c + 8 l (c < NCH), kept as raw 32-bit words (4 per
 // chunk for 16-bit types, 8 for fp32), so a row of 16-bit values costs 4 VGPRs
@@ -96,6 +111,16 @@ struct RowChunks {
       a = f16_bits_to_f32(lo);
       b = f16_bits_to_f32(hi);
     }
+  }
+  // bf16 only: round (a, b) to bf16, keep the pair as elements 2i, 2i+1 of chunk c and return the packed
+  // word (a in the low half), without unpacking the rounded values
+  __device__ __forceinline__ uint32_t put_pair_bits(int c, int i, float a, float b) {
+    static_assert(DT == kBF16, "packed bf16 pairs");
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const uint32_t p = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, bf2));  // RNE
+    w[c][i] = p;
+    return p;
   }
   // chunk c -> dst (16-byte aligned; 32 bytes for fp32)
   __device__ __forceinline__ void store_raw(int c, char* dst) const {
