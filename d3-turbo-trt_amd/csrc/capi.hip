@@ -273,7 +273,8 @@ static int gemm_impl(int mode, const void* a, int64_t lda, const float* a_scale,
     return fail(D3W8A8_EINVAL, "gemm: leading dimensions must cover the rows and be multiples of 16");
   }
   if (ldo < ncols) return fail(D3W8A8_EINVAL, "gemm: ldo must cover the output row");
-  const d3::GemmPlan plan = d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, workspace_bytes, epilogue, a_kblk, wk);
+  const d3::GemmPlan plan =
+      d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, workspace_bytes, epilogue, a_kblk, wk, base_mode(mode));
   if (plan.error) return fail(D3W8A8_EINVAL, "gemm: %s", plan.error);
   if (M == 0 || N == 0) return D3W8A8_OK;
   if (!a || !w || !out || (epilogue != D3W8A8_EPI_RAW && (!a_scale || !w_scale)))
@@ -323,7 +324,7 @@ int d3w8a8_gemm_noalloc(int mode, const void* a, int64_t lda, const float* a_sca
       tile >= D3W8A8_TILE_AUTO && tile <= D3W8A8_TILE_WS) {
     // an explicit split larger than the scratch: name both sizes rather than the generic plan error
     const d3::GemmPlan want =
-        d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, INT64_MAX, epilogue, kblk(mode), w_kblk(mode));
+        d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, INT64_MAX, epilogue, kblk(mode), w_kblk(mode), base_mode(mode));
     if (!want.error && want.ws_bytes > kScratchBytes)
       return fail(D3W8A8_EINVAL, "gemm_noalloc: ksplit %d needs %lld bytes of split-K scratch; the library holds %lld",
                   ksplit, (long long)want.ws_bytes, (long long)kScratchBytes);

@@ -115,7 +115,11 @@ int64_t rounds(int64_t tiles, int64_t cus) { return (tiles + cus - 1) / cus; }
 // 128x128 tile with 128-byte K steps, split over K by the planner (down, K = 12288: 21.8 vs 34.5 us).
 // Tile counts are weighed against the device's compute units (`cus`; the thresholds were measured on
 // 256).
-int choose_tile(int64_t M, int64_t N, int64_t K, bool fit, int epi, int64_t cus) {
+// INT8 takes the 8-wave 256x256 tile (two waves per SIMD, 128x64 accumulators in VGPRs) where the
+// 4-wave one would run: same-box, K-blocked operands, INT8 gate_up 4096 x 24576 x 4096 350.3 -> 340.5 us
+// (SwiGLU 361.2 -> 356.3), 8192 x 6144 x 4096 175.0 -> 170.8 us, single-round shapes even. FP8 keeps
+// the 4-wave tile (even on gate_up, down 141.4 against 146.3 us).
+int choose_tile(int64_t M, int64_t N, int64_t K, bool fit, int epi, int64_t cus, int mode) {
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
@@ -130,7 +134,7 @@ int choose_tile(int64_t M, int64_t N, int64_t K, bool fit, int epi, int64_t cus)
         const int64_t t192 = ((M + 255) / 256) * (N / 192);
         if (rounds(t192, cus) * 192 * 10 <= rounds(t256, cus) * 256 * 9) return kDma256x192w4;
       }
-      return kDma256w4;
+      return mode == kInt8 ? kDma256w8 : kDma256w4;
     }
     if (8 * t256x128 >= 5 * cus) {  // 160 tiles on 256 CUs
       // the same round count rule against 256x128 (ragged question batches: 1440 rows x N = 6144 is
@@ -164,12 +168,12 @@ int choose_ksplit(int64_t tiles, int nk, int bk, int64_t cus) {
 }  // namespace
 
 GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
-                   int64_t ws_bytes, int epi, bool a_kblk, bool w_kblk) {
+                   int64_t ws_bytes, int epi, bool a_kblk, bool w_kblk, int mode) {
   GemmPlan pl{};
   pl.ksplit = 1;
   const bool fit = dma_offsets_fit(M, N, K, lda, ldw, a_kblk, w_kblk);
   const int64_t cus = device_cu_count();
-  pl.tile = tile < 0 ? choose_tile(M, N, K, fit, epi, cus) : tile;
+  pl.tile = tile < 0 ? choose_tile(M, N, K, fit, epi, cus, mode) : tile;
   if (pl.tile >= kTileCount) return pl.error = "unknown tile", pl;
   if (pl.tile == kDma256x192w4 && epi == kEpiSwiGLU)
     return pl.error = "the 256x192 tile has 3 column blocks per wave; SwiGLU needs gate/up pairs", pl;

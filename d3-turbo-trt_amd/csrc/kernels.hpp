@@ -109,8 +109,9 @@ struct GemmPlan {
 };
 // `epi` (an Epilogue) rules out tiles the epilogue cannot use; a K-blocked operand (`a_kblk`,
 // `w_kblk`) rules out the register-staged tiles.
+// `mode` (kInt8 / kFp8) picks between tiles that compute the same result.
 GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
-                   int64_t ws_bytes, int epi, bool a_kblk = false, bool w_kblk = false);
+                   int64_t ws_bytes, int epi, bool a_kblk = false, bool w_kblk = false, int mode = kFp8);
 
 // Largest row capacity of a K-blocked operand: the pipelined tiles keep per-lane offsets (two K blocks
 // apart at most) below 2^32.
