@@ -153,9 +153,13 @@ __device__ __forceinline__ uint32_t quant_i8_bits(float x, const RowScale& r) {
 // 448 (1 + 2^-23), which rounds to 448 (the next E4M3 step would be 480, so
 // everything below 464 rounds down), and a NaN quotient reaches the converter
 // as a NaN (fminf / fmaxf would turn it into +-448).
+// div_row_signed is div_row's correction with the residual negated: e' = RN(q·c − x) = −e and
+// q' = RN(q − e'·r), the same value as div_row's for every x ≠ 0. For x = ±0, q = ±0, e' = +0 and
+// q' = (−0) + q keeps the sign of x, where div_row's last step turns −0 into +0 (−0 + +0).
 __device__ __forceinline__ float div_row_signed(float x, const RowScale& r) {
-  const float q = div_row(x, r);
-  return __uint_as_float((__float_as_uint(q) & 0x7fffffffu) | (__float_as_uint(x) & 0x80000000u));
+  const float q = x * r.r;
+  const float e = __builtin_fmaf(q, r.c, -x);
+  return __builtin_fmaf(-e, r.r, q);
 }
 template <bool CLAMP>
 __device__ __forceinline__ float f8_quotient(float x, const RowScale& r) {

@@ -305,19 +305,51 @@ __global__ __launch_bounds__(256) void gdn_norm_quant_vec(
     wp.get(0, wv);
   }
   const int group = head_dim >> 3;  // lanes per head
+  // Each head's rstd is computed once, not by every lane that holds a piece of it: the heads' sums of
+  // squares go to this wave's LDS slots, slot (g, c) = g * NCH + c for the head that lanes
+  // [g * group, (g + 1) * group) hold in chunk c; lanes take the slots in turn and put the rstd back.
+  __shared__ __attribute__((aligned(16))) float rstd_lds[kQuantWaves][NCH * 8];
+  float* const slots = rstd_lds[threadIdx.x >> 6];
+  const int g = lane / group;
+  {
+    float ss[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      // every lane of the wave takes part in the butterfly; lanes past the row contribute nothing used
+      float a = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a = dot2_sq<DT>(x_.w[c][i], a);
+      ss[c] = group_sum(a, group);
+    }
+    if (lane % group == 0) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) slots[g * NCH + c] = ss[c];
+    }
+  }
+  // the LDS operations of one wave complete in order; the fences keep the compiler from moving the
+  // reads of other lanes' slots ahead of the writes
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  {
+    // head_dim is a power of two, so ss * (1 / head_dim) is ss / head_dim bit for bit
+    const float inv_hd = 1.0f / (float)head_dim;
+    const int nslots = NCH * (512 / head_dim);
+    for (int j = lane; j < nslots; j += 64) {
+      const float t = slots[j] * inv_hd + eps;
+      slots[j] = 1.0f / sqrtf(t);  // torch.rsqrt on the CPU: 1 / sqrt(t), each step correctly rounded
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   RC y;
   float amax = 0.0f;
+  Bf16PairAmax am16;  // bf16: the amax of the rounded outputs, taken on the packed pairs
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    // every lane of the wave takes part in the butterfly; lanes past the row contribute nothing used
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ss = dot2_sq<DT>(x_.w[c][i], ss);
-    ss = group_sum(ss, group);
     if (RC::valid(c, lane, K)) {
-      const float var = ss / (float)head_dim;
-      const float t = var + eps;
-      const float rstd = 1.0f / sqrtf(t);  // torch.rsqrt on the CPU: 1 / sqrt(t), each step correctly rounded
+      const float rstd = slots[g * NCH + c];
       float v[8], zv[8];
       x_.get(c, v);
       z_.get(c, zv);
@@ -334,11 +366,16 @@ __global__ __launch_bounds__(256) void gdn_norm_quant_vec(
         const float d0 = 1.0f + e0, d1 = 1.0f + e1;
         const float s0 = zv[i] * __builtin_amdgcn_rcpf(d0), s1 = zv[i + 1] * __builtin_amdgcn_rcpf(d1);
         float p0 = h0 * s0, p1 = h1 * s1;
-        y.put_pair(c, i / 2, p0, p1);
-        amax = amax_acc(amax_acc(amax, p0), p1);
+        if constexpr (DT == kBF16) {
+          am16.add(y.put_pair_bits(c, i / 2, p0, p1));
+        } else {
+          y.put_pair(c, i / 2, p0, p1);
+          amax = amax_acc(amax_acc(amax, p0), p1);
+        }
       }
     }
   }
+  if constexpr (DT == kBF16) amax = am16.value();
   const RowScale s = scale_from_amax<MODE>(wave_max(amax));
   if constexpr (NCH > 12) y.fence();
   char* qr = qd.row(row);

@@ -263,11 +263,16 @@ __global__ __launch_bounds__(256) void gate_quant_vec(const void* __restrict__ x
   x_.load((const char*)x + row * ldx * RC::kES, K, lane);
   {
     const char* grow = (const char*)gate + row * ldg * RC::kES;
+    // (k / hd) * 2 hd + hd + k % hd = k + hd * (k / hd + 1), with k / hd = umulhi(k, m),
+    // m = floor((2^32 - 1) / hd) + 1: exact for k < 2^16 and 8 <= hd < 2^16 (K <= kMaxVecK), since
+    // k * m / 2^32 exceeds k / hd by less than k / 2^32 <= 2^-16 < 1 / hd
+    const uint32_t hd = (uint32_t)head_dim;
+    const uint32_t m = hd ? 0xffffffffu / hd + 1u : 0u;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const int64_t k = FULL ? RC::col(c, lane) : min(RC::col(c, lane), K - 8);
-      const int64_t gk = head_dim ? (k / head_dim) * 2 * head_dim + head_dim + k % head_dim : k;
-      const uint4 t = *(const uint4*)(grow + gk * RC::kES);
+      const uint32_t k = (uint32_t)(FULL ? RC::col(c, lane) : min(RC::col(c, lane), K - 8));
+      const uint32_t gk = hd ? k + hd * (__umulhi(k, m) + 1u) : k;
+      const uint4 t = *(const uint4*)(grow + (int64_t)gk * RC::kES);
       g_.w[c][0] = t.x;
       g_.w[c][1] = t.y;
       g_.w[c][2] = t.z;
@@ -276,6 +281,7 @@ __global__ __launch_bounds__(256) void gate_quant_vec(const void* __restrict__ x
   }
   RC y;
   float amax = 0.0f;
+  Bf16PairAmax am16;  // bf16: the amax of the rounded products, taken on the packed pairs
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     if (RC::valid(c, lane, K)) {
@@ -290,11 +296,16 @@ __global__ __launch_bounds__(256) void gate_quant_vec(const void* __restrict__ x
         float s1 = __builtin_amdgcn_rcpf(1.0f + __expf(-gv[i + 1]));
         round_pair_to<DT>(s0, s1);  // torch.sigmoid's output in the tensor dtype
         float p0 = v[i] * s0, p1 = v[i + 1] * s1;
-        y.put_pair(c, i / 2, p0, p1);
-        amax = amax_acc(amax_acc(amax, p0), p1);
+        if constexpr (DT == kBF16) {
+          am16.add(y.put_pair_bits(c, i / 2, p0, p1));
+        } else {
+          y.put_pair(c, i / 2, p0, p1);
+          amax = amax_acc(amax_acc(amax, p0), p1);
+        }
       }
     }
   }
+  if constexpr (DT == kBF16) amax = am16.value();
   const RowScale s = scale_from_amax<MODE>(wave_max(amax));
   char* qr = qd.row(row);
   char* yr = y_out ? (char*)y_out + row * ldy * RC::kES : nullptr;

@@ -1,7 +1,8 @@
 /* Checks the FMA-refined quotient the quantize kernels use instead of an fp32
  * division per element:
- *   r = RN(1 / s);  q = RN(x * r);  e = RN(x - q * s) (one FMA, exact);
- *   q' = RN(e * r + q) (one FMA), with the sign of x put back on a zero q'.
+ *   r = RN(1 / s);  q = RN(x * r);  e' = RN(q * s - x) (one FMA, exact);
+ *   q' = RN(q - e' * r) (one FMA). With the residual negated, a zero x keeps its
+ *   sign: q = +-0, e' = +0 and q' = -0 + q (x - q * s would give +0 + -0 = +0).
  * Claim: q' == RN(x / s) bit for bit whenever |x| >= 2^-100 and x / s is a
  * normal float (Markstein's correction step: r is the correctly rounded
  * reciprocal, q is within one ulp of x / s, and the residual e is exact
@@ -22,11 +23,11 @@
 static float f_of(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 static uint32_t u_of(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 
-static float div_fma(float x, float s, float r) {
+/* c = s, or 0 for an infinite s (the kernels' correction multiplier) */
+static float div_fma(float x, float c, float r) {
   const float q = x * r;
-  const float e = fmaf(-q, s, x);
-  const float q1 = fmaf(e, r, q);
-  return f_of((u_of(q1) & 0x7fffffffu) | (u_of(x) & 0x80000000u));
+  const float e = fmaf(q, c, -x);
+  return fmaf(-e, r, q);
 }
 
 static uint64_t rng_state = 0x9E3779B97F4A7C15ull;
@@ -39,9 +40,10 @@ static long long checked = 0, bad = 0;
 
 static void check(float x, float s) {
   const float want = x / s;
-  const float got = div_fma(x, s, 1.0f / s);
+  const float got = div_fma(x, isinf(s) ? 0.0f : s, 1.0f / s);
   if (!isfinite(want) || fabsf(want) > 0x1p100f) return;  /* quantized rows keep |x / s| <= 448 */
   ++checked;
+  if (signbit(got) != signbit(x)) ++bad;  /* x / s has the sign of x, zeros included (-0 -> 0x80) */
   if (fabsf(x) >= 0x1p-100f && fabsf(want) >= 0x1p-126f) {
     if (u_of(got) != u_of(want)) ++bad;
   } else if (fabsf(x) < 0x1p-100f) {
@@ -53,7 +55,7 @@ static void check(float x, float s) {
 int main(void) {
   float scales[8192];
   int ns = 0;
-  scales[ns++] = 1.0f; scales[ns++] = 0x1p-20f; scales[ns++] = 1e-12f / 127.0f; scales[ns++] = 1e-12f / 448.0f;
+  scales[ns++] = 1.0f; scales[ns++] = 0x1p-20f; scales[ns++] = INFINITY; scales[ns++] = 1e-12f / 127.0f; scales[ns++] = 1e-12f / 448.0f;
   for (int e = -40; e < 40; e += 3) {
     scales[ns++] = ldexpf(1.9999999f, e);
     scales[ns++] = ldexpf(1.0000001f, e);

@@ -60,10 +60,13 @@ def test_gate_known_values(dev):
         assert torch.equal(y.cpu(), R.gated_input(out, gate))
 
 
-@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("head_dim,Kd", [(64, 2048), (128, 2048), (256, 2048), (96, 1920), (200, 4000),
+                                         (192, 12288), (8, 16384)])
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
-def test_gate_in_place_from_q_proj_layout(dev, head_dim, mode):
-    M, Kd = 50, 2048
+def test_gate_in_place_from_q_proj_layout(dev, head_dim, Kd, mode):
+    """Heads that do not divide 512 (96, 200, 192) and the longest rows check the kernel's
+    multiply-high column mapping against the gate passed as its own tensor."""
+    M = 50
     g = gen(head_dim)
     q_proj_out = (torch.randn(M, 2 * Kd, generator=g) * 3).to(torch.bfloat16)
     out = R.outlier_activations(g, M, Kd)

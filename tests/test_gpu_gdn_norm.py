@@ -30,7 +30,7 @@ def _case(seed, M, heads, hd, wdtype=torch.bfloat16, dtype=torch.bfloat16):
 
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
 @pytest.mark.parametrize("M,heads,hd", [(1, 1, 128), (37, 32, 128), (130, 8, 64), (64, 16, 256), (9, 24, 512),
-                                        (20, 5, 128)])
+                                        (20, 5, 128), (6, 256, 64), (5, 40, 64)])
 def test_gdn_norm_quantize_matches_oracle(dev, mode, M, heads, hd):
     x, z, w = _case(M * 3 + heads + hd, M, heads, hd)
     q, s, y = K.gdn_norm_quantize(x.to(dev), z.to(dev), w.to(dev), 1e-6, hd, mode, want_y=True)

@@ -118,6 +118,38 @@ def test_fp8_int8_quotient_just_above_the_code_range(dev, mode):
     assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8))
 
 
+@pytest.mark.parametrize("kblock", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_fp8_zero_codes_keep_the_sign(dev, dtype, kblock):
+    """x / scale is a zero of x's sign for x = +-0, and e4m3fn keeps it: -0 -> 0x80, +0 -> 0x00
+    (quant.py:98). The gated and GDN kernels quantize their own outputs the same way."""
+    g = gen(77)
+    M, Kd = 8, 4096
+    x = R.outlier_activations(g, M, Kd).to(dtype)
+    x[:, 0::3] = -0.0
+    x[:, 1::7] = 0.0
+    q_ref, s_ref = R.quantize_rows(x, "fp8")
+    assert int((q_ref.view(torch.uint8) == 0x80).sum()) > M * Kd // 4
+    q, s = K.quantize_rows(x.to(dev), "fp8", kblock=kblock)
+    q = K.unblock(q) if kblock else q
+    assert torch.equal(s.cpu(), s_ref)
+    assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8))
+    if dtype != torch.float32:
+        gate = torch.randn(M, Kd, generator=g).to(dtype)
+        q, s, y = K.gate_quantize(x.to(dev), gate.to(dev), "fp8", want_y=True, kblock=kblock)
+        q = K.unblock(q) if kblock else q
+        q_ref, s_ref = R.quantize_rows(y.cpu(), "fp8")
+        assert int((q_ref.view(torch.uint8) == 0x80).sum()) > M * Kd // 8
+        assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8)) and torch.equal(s.cpu(), s_ref)
+        w = (1 + 0.1 * torch.randn(128, generator=g)).to(dtype)
+        q, s, y = K.gdn_norm_quantize(x.to(dev), gate.to(dev), w.to(dev), 1e-6, 128, "fp8", want_y=True,
+                                      kblock=kblock)
+        q = K.unblock(q) if kblock else q
+        q_ref, s_ref = R.quantize_rows(y.cpu(), "fp8")
+        assert int((q_ref.view(torch.uint8) == 0x80).sum()) > M * Kd // 16
+        assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8)) and torch.equal(s.cpu(), s_ref)
+
+
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
 def test_non_finite_rows_keep_nan_scale(dev, mode):
     """A NaN in a row makes the reference's amax, scale and linear output NaN (x.abs().amax() and
