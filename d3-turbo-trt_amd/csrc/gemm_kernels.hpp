@@ -606,21 +606,26 @@ __device__ __forceinline__ void splitk_store(const GemmParams& p, ACC (&acc)[TM]
                        __builtin_bit_cast(uint32_t, (E)acc[i][j][4 * g + 2]), __builtin_bit_cast(uint32_t, (E)acc[i][j][4 * g + 3]));
 }
 
-// Split-K, second half (its own launch, so the slots are visible device-wide):
-// one wave per 32-row block of a GEMM wave's sub-tile sums the ksplit slots in
-// split order 0, 1, ..., ksplit-1 (a fixed floating-point order: results do not
-// depend on scheduling) and runs the same epilogue the unsplit kernel runs.
-// Spreading the sum over tiles x NW x TM small workgroups keeps every CU
-// reading instead of one workgroup per tile.
+// Split-K, second half (its own launch, so the slots are visible device-wide).
+// One workgroup per 32-row block of a GEMM wave's sub-tile (tiles x NW x TM
+// workgroups, so every CU reads) runs the same epilogue the unsplit kernel
+// runs, on the sum of the ksplit slots. Its kSumWaves waves load the slots
+// at once: wave r sums splits r, r + kSumWaves, ... in increasing order, and
+// wave 0 adds the other waves' sums, taken through LDS, in wave order. The
+// floating-point order is fixed (results do not depend on scheduling), and all
+// the slots' loads are in flight together: one wave taking the splits two at a
+// time waited for ksplit / 2 round trips.
+constexpr int kSumWaves = 4;
 template <int MODE, int BM, int BN, int WM, int WN, int EPI, int OUT>
-__global__ __launch_bounds__(64) void gemm_splitk_reduce(GemmParams p) {
+__global__ __launch_bounds__(64 * kSumWaves) void gemm_splitk_reduce(GemmParams p) {
   using MF = Mfma<MODE>;
   typedef typename MF::acc acc_t;
   using E = typename std::conditional<MODE == kInt8, int, float>::type;
   constexpr int NW = WM * WN, WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   constexpr int WAVE_U4 = splitk_wave_words<NW, TM, TN>(), TILE_U4 = NW * WAVE_U4;
   __shared__ __attribute__((aligned(16))) uint8_t lds[EpiLds<TN, EPI, OUT>::BYTES];
-  const int lane = threadIdx.x;
+  __shared__ uint4 sums[kSumWaves - 1][TN * 4][64];  // waves 1.. : lane-contiguous, 1 KiB per store
+  const int lane = threadIdx.x & 63, r = threadIdx.x >> 6;
   int b = (int)blockIdx.x;
   const int i = b % TM;
   b /= TM;
@@ -634,23 +639,40 @@ __global__ __launch_bounds__(64) void gemm_splitk_reduce(GemmParams p) {
 #pragma unroll
   for (int j = 0; j < TN; ++j)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[0][j][r] = 0;
+    for (int e = 0; e < 16; ++e) acc[0][j][e] = 0;
+  auto add4 = [&](int j, int g, const uint4 v) {
+    acc[0][j][4 * g] = (E)acc[0][j][4 * g] + __builtin_bit_cast(E, v.x);
+    acc[0][j][4 * g + 1] = (E)acc[0][j][4 * g + 1] + __builtin_bit_cast(E, v.y);
+    acc[0][j][4 * g + 2] = (E)acc[0][j][4 * g + 2] + __builtin_bit_cast(E, v.z);
+    acc[0][j][4 * g + 3] = (E)acc[0][j][4 * g + 3] + __builtin_bit_cast(E, v.w);
+  };
 #pragma unroll 2
-  for (int s = 0; s < S; ++s) {
+  for (int s = r; s < S; s += kSumWaves) {
     uint4 u[TN * 4];
 #pragma unroll
     for (int w = 0; w < TN * 4; ++w) u[w] = src[(int64_t)s * TILE_U4 + w * 64];
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const uint4 v = u[j * 4 + g];
-        acc[0][j][4 * g] = (E)acc[0][j][4 * g] + __builtin_bit_cast(E, v.x);
-        acc[0][j][4 * g + 1] = (E)acc[0][j][4 * g + 1] + __builtin_bit_cast(E, v.y);
-        acc[0][j][4 * g + 2] = (E)acc[0][j][4 * g + 2] + __builtin_bit_cast(E, v.z);
-        acc[0][j][4 * g + 3] = (E)acc[0][j][4 * g + 3] + __builtin_bit_cast(E, v.w);
-      }
+      for (int g = 0; g < 4; ++g) add4(j, g, u[j * 4 + g]);
   }
+  if (r > 0 && r < S) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        sums[r - 1][j * 4 + g][lane] =
+            make_uint4(__builtin_bit_cast(uint32_t, (E)acc[0][j][4 * g]), __builtin_bit_cast(uint32_t, (E)acc[0][j][4 * g + 1]),
+                       __builtin_bit_cast(uint32_t, (E)acc[0][j][4 * g + 2]), __builtin_bit_cast(uint32_t, (E)acc[0][j][4 * g + 3]));
+  }
+  __syncthreads();
+  if (r != 0) return;  // no barrier follows: the epilogue is wave-local
+  const int nsum = S < kSumWaves ? S : kSumWaves;
+  for (int q = 1; q < nsum; ++q)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) add4(j, g, sums[q - 1][j * 4 + g][lane]);
   epilogue<MODE, 1, TN, EPI, OUT>(p, acc, (int64_t)tm * BM + wm * WTM + i * 32, (int64_t)tn * BN + wn * WTN, lane, lds);
 }
 
@@ -963,7 +985,7 @@ static hipError_t launch_dma(GemmParams p, hipStream_t st) {
     if (e != hipSuccess) return e;
     constexpr int WAVE_BLOCKS = WM * WN * (BM / WM / 32);  // reduce workgroups per tile
     hipLaunchKernelGGL((gemm_splitk_reduce<MODE, BM, BN, WM, WN, EPI, OUT>), dim3((unsigned)(tiles * WAVE_BLOCKS)),
-                       dim3(64), 0, st, p);
+                       dim3(64 * kSumWaves), 0, st, p);
   }
   return hipGetLastError();
 }

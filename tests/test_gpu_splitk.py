@@ -1,7 +1,7 @@
 """GPU parity: split-K GEMMs (d3w8a8_gemm_ws) for the skinny question-pass shapes.
 
 Split-K hands each output tile's K range to several workgroups and adds their
-partial accumulators in split order. INT8 must equal the exact integer product
+partial accumulators in a fixed order. INT8 must equal the exact integer product
 and the unsplit GEMM bit for bit, for every epilogue; FP8 must be reproducible
 (same split, same bits) and within the FP8 accumulator bound of the oracle.
 The partial sums live in a per-stream workspace between the two launches of a
