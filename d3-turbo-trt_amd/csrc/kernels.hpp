@@ -50,7 +50,7 @@ struct GemmParams {
   // Split-K (pipelined tiles only): ksplit workgroups share one output tile,
   // each over a contiguous range of K steps, and store their raw accumulators
   // in `partial` (ksplit tile-sized slots per tile); a second launch sums the
-  // slots in split order and runs the epilogue.
+  // slots in a fixed order and runs the epilogue.
   int ksplit;
   uint32_t* partial;  // tiles * ksplit * BM * BN 32-bit words
 };
