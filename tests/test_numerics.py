@@ -2,11 +2,14 @@
 
 1. The FMA-refined quotient q' = RN(RN(x - q s) r + q), q = RN(x r), r = RN(1 / s), equals RN32(x / s)
    (quant.py:100 divides) for every bf16 x and random fp32 x over ~900 row scales, and rounds to the same
-   integer everywhere (tests/c/fma_division.c, compiled here with gcc and FMA from libm).
+   integer everywhere; its FP8 form with the residual negated keeps the sign of every quotient, zeros
+   included (tests/c/fma_division.c, compiled here with gcc and FMA from libm).
 2. clamp(v, -127, 127) + 1.5 * 2^23 leaves clamp(rint(v), -127, 127) in the low byte of the float bits
    (torch.round is half-to-even; quant.py:100 rounds, then clamps).
 3. With scale = RN(amax / 127) and |x| <= amax, RN(x / scale) rounds to at most 127: the int8 clamp never
    acts when the amax comes from the quantized values themselves.
+4. The gated kernel's 32-bit column mapping: umulhi(k, floor((2^32 - 1) / hd) + 1) == k // hd for every
+   row column k < 2^14 (the longest row) and every head width hd = 8, 16, ..., 2^14.
 """
 
 from __future__ import annotations
@@ -58,3 +61,12 @@ def test_magic_add_rounds_half_to_even_then_clamps():
     c = np.clip(v, np.float32(-127.0), np.float32(127.0)).astype(np.float32)
     got = ((c + np.float32(12582912.0)).view(np.uint32) & 0xFF).astype(np.uint8).view(np.int8)
     assert np.array_equal(got, want)
+
+
+def test_gate_column_division_by_multiply_high():
+    k = np.arange(1 << 14, dtype=np.uint64)
+    for hd in range(8, (1 << 14) + 1, 8):
+        m = np.uint64((0xFFFFFFFF // hd + 1) & 0xFFFFFFFF)
+        assert m != 0
+        q = (k * m) >> np.uint64(32)
+        assert np.array_equal(q, k // np.uint64(hd)), hd
