@@ -14,6 +14,7 @@
 #include "../../include/d3w8a8.h"
 
 static_assert(d3::kMaxSegments == D3W8A8_MAX_SEGMENTS, "segment limit of the C ABI and the kernels");
+static_assert(d3::kTileCount == D3W8A8_TILE_LAST + 1, "tile codes of the C ABI and the planner");
 
 namespace {
 
@@ -247,7 +248,7 @@ static int gemm_impl(int mode, const void* a, int64_t lda, const float* a_scale,
   if (epilogue < D3W8A8_EPI_DEQUANT || epilogue > D3W8A8_EPI_RESIDUAL)
     return fail(D3W8A8_EINVAL, "gemm: unknown epilogue %d", epilogue);
   if (epilogue != D3W8A8_EPI_RAW && !dtype_ok(out_dtype)) return fail(D3W8A8_EINVAL, "gemm: unknown out dtype");
-  if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_WS) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
+  if (tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_LAST) return fail(D3W8A8_EINVAL, "gemm: unknown tile %d", tile);
   if (ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) return fail(D3W8A8_EINVAL, "gemm: bad ksplit %d", ksplit);
   if (workspace_bytes < 0 || (workspace_bytes > 0 && (!workspace || !aligned(workspace, 256))))
     return fail(D3W8A8_EINVAL, "gemm: the workspace must be 256-byte aligned device memory");
@@ -321,7 +322,7 @@ int d3w8a8_gemm_noalloc(int mode, const void* a, int64_t lda, const float* a_sca
                         int ksplit, void* stream) {
   if (ksplit > 1 && M > 0 && N > 0 && K > 0 && K % 16 == 0 && (kblk(mode) ? lda >= M : lda >= K) &&
       (w_kblk(mode) ? ldw >= N : ldw >= K) && M <= INT32_MAX / 2 && N <= INT32_MAX / 2 &&
-      tile >= D3W8A8_TILE_AUTO && tile <= D3W8A8_TILE_WS) {
+      tile >= D3W8A8_TILE_AUTO && tile <= D3W8A8_TILE_LAST) {
     // an explicit split larger than the scratch: name both sizes rather than the generic plan error
     const d3::GemmPlan want =
         d3::plan_gemm(M, N, K, lda, ldw, tile, ksplit, INT64_MAX, epilogue, kblk(mode), w_kblk(mode), base_mode(mode));
@@ -338,7 +339,7 @@ int d3w8a8_gemm_noalloc(int mode, const void* a, int64_t lda, const float* a_sca
 int64_t d3w8a8_gemm_workspace(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, int tile, int ksplit,
                               int64_t max_bytes) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 16 || lda < K || ldw < K || M > INT32_MAX / 2 || N > INT32_MAX / 2 ||
-      tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_WS || ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) {
+      tile < D3W8A8_TILE_AUTO || tile > D3W8A8_TILE_LAST || ksplit < D3W8A8_KSPLIT_AUTO || ksplit == 0) {
     fail(D3W8A8_EINVAL, "gemm_workspace: bad arguments");
     return -1;
   }

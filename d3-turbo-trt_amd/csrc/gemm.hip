@@ -80,6 +80,8 @@ TileShape shape_of(int tile) {
     case kDma128w4k128: return {128, 128, true, 128};
     case kDma256x192w4: return {256, 192, true, 64};
     case kWs: return {128, 32, true, 128};
+    case kDma192x192w4: return {192, 192, true, 64};
+    case kDma192x128w4: return {192, 128, true, 64};
   }
   return {0, 0, false, 0};
 }
@@ -119,6 +121,24 @@ int64_t rounds(int64_t tiles, int64_t cus) { return (tiles + cus - 1) / cus; }
 // 4-wave one would run: same-box, K-blocked operands, INT8 gate_up 4096 x 24576 x 4096 350.3 -> 340.5 us
 // (SwiGLU 361.2 -> 356.3), 8192 x 6144 x 4096 175.0 -> 170.8 us, single-round shapes even. FP8 keeps
 // the 4-wave tile (even on gate_up, down 141.4 against 146.3 us).
+// A 192-row tile in place of the chosen 256-row one where its rounds x tile area is at least 10%
+// below the chosen tile's (ragged batches whose 256-row tiles leave part of a round idle: 1440 rows are
+// 6 tile rows of 256, 192 tiles at N = 4096 or 6144, but 8 tile rows of 192, one whole round).
+// The larger of two equal-cost tiles stays.
+int prefer_192_rows(int tile, int64_t cost, int64_t M, int64_t N, int epi, int64_t cus) {
+  const int64_t tm = (M + 191) / 192;
+  const int64_t bar = cost * 9;
+  int best = tile;
+  int64_t best_cost = cost;
+  if (epi != kEpiSwiGLU && N % 192 == 0) {
+    const int64_t c = rounds(tm * (N / 192), cus) * 192 * 192;
+    if (c * 10 <= bar && c < best_cost) best = kDma192x192w4, best_cost = c;
+  }
+  const int64_t c = rounds(tm * ((N + 127) / 128), cus) * 192 * 128;
+  if (c * 10 <= bar && c < best_cost) best = kDma192x128w4;
+  return best;
+}
+
 int choose_tile(int64_t M, int64_t N, int64_t K, bool fit, int epi, int64_t cus, int mode) {
   const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
   const int64_t t256x128 = ((M + 255) / 256) * ((N + 127) / 128);
@@ -132,18 +152,20 @@ int choose_tile(int64_t M, int64_t N, int64_t K, bool fit, int epi, int64_t cus,
     if (4 * t256 >= 3 * cus) {  // 192 tiles on 256 CUs
       if (epi != kEpiSwiGLU && N % 192 == 0) {
         const int64_t t192 = ((M + 255) / 256) * (N / 192);
-        if (rounds(t192, cus) * 192 * 10 <= rounds(t256, cus) * 256 * 9) return kDma256x192w4;
+        if (rounds(t192, cus) * 192 * 10 <= rounds(t256, cus) * 256 * 9)
+          return prefer_192_rows(kDma256x192w4, rounds(t192, cus) * 256 * 192, M, N, epi, cus);
       }
-      return mode == kInt8 ? kDma256w8 : kDma256w4;
+      return prefer_192_rows(mode == kInt8 ? kDma256w8 : kDma256w4, rounds(t256, cus) * 256 * 256, M, N, epi, cus);
     }
     if (8 * t256x128 >= 5 * cus) {  // 160 tiles on 256 CUs
       // the same round count rule against 256x128 (ragged question batches: 1440 rows x N = 6144 is
       // 288 tiles of 256x128, one round and 32 tiles, but 192 tiles of 256x192, one round)
       if (epi != kEpiSwiGLU && N % 192 == 0) {
         const int64_t t192 = ((M + 255) / 256) * (N / 192);
-        if (rounds(t192, cus) * 192 * 10 <= rounds(t256x128, cus) * 128 * 9) return kDma256x192w4;
+        if (rounds(t192, cus) * 192 * 10 <= rounds(t256x128, cus) * 128 * 9)
+          return prefer_192_rows(kDma256x192w4, rounds(t192, cus) * 256 * 192, M, N, epi, cus);
       }
-      return kDma256x128w4;
+      return prefer_192_rows(kDma256x128w4, rounds(t256x128, cus) * 256 * 128, M, N, epi, cus);
     }
     return kDma128w4;
   }
@@ -175,8 +197,8 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw, in
   const int64_t cus = device_cu_count();
   pl.tile = tile < 0 ? choose_tile(M, N, K, fit, epi, cus, mode) : tile;
   if (pl.tile >= kTileCount) return pl.error = "unknown tile", pl;
-  if (pl.tile == kDma256x192w4 && epi == kEpiSwiGLU)
-    return pl.error = "the 256x192 tile has 3 column blocks per wave; SwiGLU needs gate/up pairs", pl;
+  if ((pl.tile == kDma256x192w4 || pl.tile == kDma192x192w4) && epi == kEpiSwiGLU)
+    return pl.error = "the 192-column tiles have 3 column blocks per wave; SwiGLU needs gate/up pairs", pl;
   const TileShape sh = shape_of(pl.tile);
   if ((a_kblk || w_kblk) && !sh.dma) return pl.error = "a K-blocked operand needs a pipelined (DMA) tile", pl;
   if (sh.dma && K % sh.bk != 0)

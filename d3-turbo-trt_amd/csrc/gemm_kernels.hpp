@@ -1012,6 +1012,10 @@ hipError_t launch_epi(GemmParams p, int tile, hipStream_t st) {
       if constexpr (EPI == kEpiSwiGLU) return hipErrorInvalidValue;  // 3 column blocks per wave: no gate/up pairs
       else return launch_dma<MODE, 256, 192, 2, 2, EPI, OUT>(p, st);
     case kWs: return launch_ws<MODE, EPI, OUT>(p, st);
+    case kDma192x192w4:
+      if constexpr (EPI == kEpiSwiGLU) return hipErrorInvalidValue;  // 3 column blocks per wave: no gate/up pairs
+      else return launch_dma<MODE, 192, 192, 2, 2, EPI, OUT>(p, st);
+    case kDma192x128w4: return launch_dma<MODE, 192, 128, 2, 2, EPI, OUT>(p, st);
   }
   return hipErrorInvalidValue;
 }

@@ -94,7 +94,9 @@ enum TileCfg : int {
   kDma128w4k128 = 7, // DMA pipeline 128x128, 4 waves, 128-byte K steps (weight streaming, K % 128 == 0)
   kDma256x192w4 = 8, // DMA pipeline 256x192, 4 waves (128x96 each), 4 stages; not for SwiGLU
   kWs = 9,           // weight streaming for skinny M: 32- or 64-column slabs, waves split K (K % 128 == 0)
-  kTileCount = 10
+  kDma192x192w4 = 10, // DMA pipeline 192x192, 4 waves (96x96 each), 4 stages; not for SwiGLU
+  kDma192x128w4 = 11, // DMA pipeline 192x128, 4 waves (96x64 each), 4 stages
+  kTileCount = 12
 };
 
 constexpr int kMaxKSplit = 32;

@@ -30,10 +30,13 @@ TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4 = 3, 4, 5
 TILE_DMA_128_W4_K128 = 7  # 128-byte K steps: K % 128 == 0
 TILE_DMA_256x192_W4 = 8  # 3 column blocks per wave: not for the SwiGLU epilogue
 TILE_WS = 9  # weight streaming for skinny M: K % 128 == 0, never splits K
+TILE_DMA_192x192_W4 = 10  # 3 column blocks per wave: not for the SwiGLU epilogue
+TILE_DMA_192x128_W4 = 11
 TILES = (TILE_256, TILE_128, TILE_64x128, TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4,
-         TILE_DMA_128_W4_K128, TILE_DMA_256x192_W4, TILE_WS)
+         TILE_DMA_128_W4_K128, TILE_DMA_256x192_W4, TILE_WS, TILE_DMA_192x192_W4, TILE_DMA_192x128_W4)
 DMA_TILES = (TILE_DMA_256_W8, TILE_DMA_256_W4, TILE_DMA_128_W4, TILE_DMA_256x128_W4, TILE_DMA_128_W4_K128,
-             TILE_DMA_256x192_W4, TILE_WS)
+             TILE_DMA_256x192_W4, TILE_WS, TILE_DMA_192x192_W4, TILE_DMA_192x128_W4)
+NO_SWIGLU_TILES = (TILE_DMA_256x192_W4, TILE_DMA_192x192_W4)  # three 32-column blocks per wave
 
 
 def tile_k_multiple(tile: int) -> int:

@@ -82,6 +82,11 @@ extern "C" {
                                       * (64 with SwiGLU), one wave streams the weights, one per 32 rows
                                       * computes; no split-K workspace; K % 128 == 0; results equal
                                       * tile 7 unsplit bit for bit (so FP8 rows do not depend on M) */
+#define D3W8A8_TILE_DMA_192x192_W4 10 /* DMA 192x192, 4 waves: whole rounds for ragged batches whose
+                                       * 256-row tiles leave part of one idle (1440 rows, N = 6144);
+                                       * not with D3W8A8_EPI_SWIGLU */
+#define D3W8A8_TILE_DMA_192x128_W4 11 /* DMA 192x128, 4 waves (1440 rows, N = 4096) */
+#define D3W8A8_TILE_LAST D3W8A8_TILE_DMA_192x128_W4
 
 const char* d3w8a8_version(void);
 const char* d3w8a8_last_error(void);

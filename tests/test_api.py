@@ -175,11 +175,12 @@ def test_split_k_plan_on_the_host():
     assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, 1, 2, big) == -1  # register-staged tile
     assert b"128x128" in lib.d3w8a8_last_error()
     assert lib.d3w8a8_gemm_workspace(128, 4096, 4096, 4096, 4096, 4, 2, big) == -1  # 256x256 tile
-    # the 256x192 and weight-streaming tiles are accepted (no split), the next tile code is not
-    assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, _lib.TILE_DMA_256x192_W4, -1, big) == 0
-    assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, _lib.TILE_DMA_256x192_W4, 2, big) == -1
-    assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, _lib.TILE_WS, -1, big) == 0
-    assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, _lib.TILE_WS + 1, -1, big) == -1
+    # the 192-column, 192-row and weight-streaming tiles are accepted (no split), the next tile code is not
+    for t in (_lib.TILE_DMA_256x192_W4, _lib.TILE_WS, _lib.TILE_DMA_192x192_W4, _lib.TILE_DMA_192x128_W4):
+        assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, t, -1, big) == 0, t
+    for t in (_lib.TILE_DMA_256x192_W4, _lib.TILE_DMA_192x192_W4, _lib.TILE_DMA_192x128_W4):
+        assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, t, 2, big) == -1, t
+    assert lib.d3w8a8_gemm_workspace(4096, 6144, 4096, 4096, 4096, max(_lib.TILES) + 1, -1, big) == -1
     dummy = 256
     assert lib.d3w8a8_gemm_ws(0, dummy, 4096, dummy, dummy, 4096, dummy, 128, 4096, 4096, 0, 0, dummy, 4096,
                               None, 0, None, None, 5, 4, dummy, 1 << 20, None) == _lib.EINVAL

@@ -88,7 +88,7 @@ def test_c3_ragged_int8_full_width(dev, N):
     sep_raw = torch.cat(sep_raw)
     # packed, on the automatic tile and on every pipelined tile that takes a ragged batch of this size
     tiles = [_lib.TILE_AUTO, _lib.TILE_DMA_256_W4, _lib.TILE_DMA_256x192_W4, _lib.TILE_DMA_256x128_W4,
-             _lib.TILE_DMA_128_W4]
+             _lib.TILE_DMA_128_W4, _lib.TILE_DMA_192x192_W4, _lib.TILE_DMA_192x128_W4]
     for tile in tiles:
         raw = K.gemm("int8", q, None, wd, None, epilogue=_lib.EPI_RAW, tile=tile)
         assert torch.equal(raw, sep_raw), f"tile {tile}: packed raw accumulators differ from separate GEMMs"
