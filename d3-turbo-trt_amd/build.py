@@ -47,7 +47,9 @@ def _compile(src: str) -> str:
 
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    # the GEMM instantiation files take the longest: start them first
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")),
+                     key=lambda s: (not os.path.basename(s).startswith("gemm_"), s))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
         objs = list(ex.map(_compile, sources))
     out = os.path.join(PKG, "libd3w8a8.so")

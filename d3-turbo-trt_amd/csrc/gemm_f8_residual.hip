@@ -1,8 +1,6 @@
-// Instantiations: f8 GEMM, residual epilogue.
+// Instantiations: f8 GEMM, residual epilogue, bf16 output.
 #include "gemm_kernels.hpp"
 
 namespace d3 {
 template hipError_t launch_epi<kFp8, kEpiResidual, kBF16>(GemmParams, int, hipStream_t);
-template hipError_t launch_epi<kFp8, kEpiResidual, kF16>(GemmParams, int, hipStream_t);
-template hipError_t launch_epi<kFp8, kEpiResidual, kF32>(GemmParams, int, hipStream_t);
 }  // namespace d3

@@ -1,9 +1,7 @@
-// Instantiations: i8 GEMM, raw and dequant epilogues.
+// Instantiations: i8 GEMM, raw accumulators and fp32 dequant.
 #include "gemm_kernels.hpp"
 
 namespace d3 {
 template hipError_t launch_epi<kInt8, kEpiRaw, kF32>(GemmParams, int, hipStream_t);
-template hipError_t launch_epi<kInt8, kEpiDequant, kBF16>(GemmParams, int, hipStream_t);
-template hipError_t launch_epi<kInt8, kEpiDequant, kF16>(GemmParams, int, hipStream_t);
 template hipError_t launch_epi<kInt8, kEpiDequant, kF32>(GemmParams, int, hipStream_t);
 }  // namespace d3

@@ -1,0 +1,7 @@
+// Instantiations: i8 GEMM, residual epilogue, fp16 and fp32 outputs.
+#include "gemm_kernels.hpp"
+
+namespace d3 {
+template hipError_t launch_epi<kInt8, kEpiResidual, kF16>(GemmParams, int, hipStream_t);
+template hipError_t launch_epi<kInt8, kEpiResidual, kF32>(GemmParams, int, hipStream_t);
+}  // namespace d3

@@ -1,8 +1,6 @@
-// Instantiations: i8 GEMM, swiglu epilogue.
+// Instantiations: i8 GEMM, SwiGLU epilogue, bf16 output.
 #include "gemm_kernels.hpp"
 
 namespace d3 {
 template hipError_t launch_epi<kInt8, kEpiSwiGLU, kBF16>(GemmParams, int, hipStream_t);
-template hipError_t launch_epi<kInt8, kEpiSwiGLU, kF16>(GemmParams, int, hipStream_t);
-template hipError_t launch_epi<kInt8, kEpiSwiGLU, kF32>(GemmParams, int, hipStream_t);
 }  // namespace d3

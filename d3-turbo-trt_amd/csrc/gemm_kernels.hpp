@@ -972,7 +972,9 @@ static hipError_t launch_dma(GemmParams p, hipStream_t st) {
   p.tiles_m = (int)((p.M + BM - 1) / BM);
   p.tiles_n = (int)((p.N + BN - 1) / BN);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
-  if constexpr (PersistLayout<MODE, BM, BN, WM, WN, EPI, OUT, BK>::value) {
+  // the walk is built for the 256-row tiles it was measured on; the 192-row tiles always run one
+  // workgroup per tile (fewer kernels to compile)
+  if constexpr (PersistLayout<MODE, BM, BN, WM, WN, EPI, OUT, BK>::value && BM == 256) {
     // one workgroup per CU; a multiple of the 8 XCDs keeps each workgroup's tiles on its own XCD
     const int64_t cus = device_cu_count() & ~7;
     if (gemm_persistent() && cus >= 8 && tiles > cus) {

@@ -37,8 +37,7 @@ def _operands(g, N, mode):
 
 
 @pytest.mark.parametrize("tile,N", [(_lib.TILE_AUTO, 7936), (_lib.TILE_DMA_256_W4, 7936),
-                                    (_lib.TILE_DMA_256x192_W4, 6144), (_lib.TILE_DMA_256x128_W4, 4096),
-                                    (_lib.TILE_DMA_192x192_W4, 6144), (_lib.TILE_DMA_192x128_W4, 4096)])
+                                    (_lib.TILE_DMA_256x192_W4, 6144), (_lib.TILE_DMA_256x128_W4, 4096)])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
 def test_int8_dequant_many_tiles(dev, tile, N, out_dtype):
     q, s, wq, ws = _operands(gen(N + tile), N, "int8")
