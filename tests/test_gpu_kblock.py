@@ -197,6 +197,29 @@ def test_ragged_kblock(dev, mode, lengths):
 
 
 @pytest.mark.parametrize("mode", ["int8", "fp8"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("lengths,W,H", [([0, 7, 1, 0, 13], 13, 4096), ([3] * 40, 5, 512),
+                                         ([1, 119, 57], 119, 12288), ([2, 0], 4, 64)])
+def test_ragged_kblock_pairs(dev, mode, dtype, lengths, W, H):
+    """The ragged gather into a K-blocked q against the row-major one: empty segments first and in
+    between, odd totals, every input dtype, short and long rows, with and without the zeroed output."""
+    g = gen(len(lengths) * 131 + W + H)
+    B, N = len(lengths), 64
+    x = R.outlier_activations(g, B * W, H).to(dtype).reshape(B, W, H).to(dev)
+    print(f"ragged pairs {mode} {dtype} lengths={lengths} W={W} H={H}", flush=True)
+    for with_out in (False, True):
+        res = []
+        for kb in (False, True):
+            out = torch.full((B * W, N), 3.0, dtype=torch.bfloat16, device=dev) if with_out else None
+            q, s, rm = K.quantize_rows_ragged(x, lengths, mode, out=out, kblock=kb)
+            res.append((K.unblock(q) if kb else q, s, rm, out))
+        (q, s, rm, o), (qk, sk, rmk, ok) = res
+        assert same_bytes(qk, q) and torch.equal(sk, s) and torch.equal(rmk, rm)
+        if with_out:
+            assert torch.equal(ok, o)
+
+
+@pytest.mark.parametrize("mode", ["int8", "fp8"])
 def test_modules_kblock_equal_row_major(dev, mode):
     """QuantLinear.forward / forward_ragged, the MLP block and a stack layer: the K-blocked hand-off between
     quantize and GEMM (the default where K % 64 == 0) returns what the row-major one does."""
